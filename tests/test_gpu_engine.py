@@ -1,0 +1,285 @@
+"""End-to-end parity of the HIP engine against the oracle engine (tread/engine.py restated on CPU).
+
+Same seeded random-init weights (bf16) in both; the oracle runs the reference's torch op sequence
+on the CPU in bf16. Checked per request: block keys, hit/miss/token accounting and recompute_eff
+identical; assembled-cache layout bit-exact (V, delta-0 rows) and K within 1 bf16 ulp of the fp32
+rotation of the same blocks; first-token logits within KL 1e-4 of the oracle's; the deviation
+selection equal to the oracle's except for candidates whose oracle score lies within 2 bf16 ulps
+of the selection threshold (scores are bf16, so upstream rounding differences can reorder only
+those). Re-expresses tests/test_engine.py:46-178 of the reference with random-init models.
+"""
+import pytest
+import torch
+
+from oracle import model_ref as M
+from oracle import tread_ref as R
+from tread_amd import Engine, BlockStore, prefill_full
+from tread_amd.model import DecoderLM, ModelConfig, synthetic_model
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+CFGS = {
+    # hd 128, G = 4, Qwen-style biases
+    "q128": ModelConfig(512, 256, 4, 8, 2, 128, 512, rope_theta=1000000.0, attention_bias=True),
+    # hd 64, G = 7 (the 0.5B / 7B group size), tied embeddings
+    "q64g7": ModelConfig(512, 448, 3, 7, 1, 64, 512, rope_theta=1000000.0, attention_bias=True,
+                         tie_word_embeddings=True),
+    # Llama-style: no biases, theta 5e5, G = 8
+    "llama": ModelConfig(512, 256, 3, 8, 1, 128, 384, rope_theta=500000.0, rms_norm_eps=1e-5,
+                         attention_bias=False, family="llama"),
+}
+
+
+def kl(a, b):
+    return R.kl(a.float().cpu(), b.float().cpu())
+
+
+def bf16_ulps(a, b):
+    def ordered(t):
+        i = t.contiguous().view(torch.int16).to(torch.int32)
+        return torch.where(i >= 0, i, -(i + 32768))
+    return (ordered(a.cpu()) - ordered(b.cpu())).abs()
+
+
+def build(name, std=0.05):
+    cfg = CFGS[name]
+    cpu = synthetic_model(cfg, "cpu", torch.bfloat16, seed=0, std=std, bias_std=0.05)
+    sd = cpu.state_dict()
+    gpu = DecoderLM(cfg, DEV, torch.bfloat16)
+    gpu.load_state_dict(sd)
+    ref = R.M.load(cfg, sd, torch.bfloat16)
+    return cfg, gpu, ref
+
+
+def request(cfg, seed=1, n_docs=4, lens=(50, 33, 70, 41), n_prefix=16, n_query=9):
+    g = torch.Generator().manual_seed(seed)
+    V = cfg.vocab_size
+    prefix = torch.randint(0, V, (n_prefix,), generator=g)
+    docs = [torch.randint(0, V, (lens[i % len(lens)],), generator=g) for i in range(n_docs)]
+    query = torch.randint(0, V, (n_query,), generator=g)
+    return prefix, docs, query
+
+
+def on(x):
+    return [t.to(DEV) for t in x] if isinstance(x, list) else x.to(DEV)
+
+
+@pytest.fixture(scope="module", params=list(CFGS))
+def setup(request):
+    return build(request.param)
+
+
+def test_keys_stats_and_logits_match_oracle_across_ratios(setup):
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg)
+    eng = Engine(gpu, BlockStore(1 << 30))
+    oeng = R.Engine(ref, R.BlockStore(1 << 30))
+    assert eng.sig == oeng.sig == ("", "torch.bfloat16", cfg.rope_theta, None)
+    # pass 1: cold, fills both stores (packed block-diagonal prefill)
+    a, _, st = eng.prefill(on(prefix), on(docs), on(query))
+    b, _, ost = oeng.prefill(prefix, docs, query)
+    assert (st.hits, st.misses, st.tokens_reused, st.tokens_prefilled) == \
+           (ost.hits, ost.misses, ost.tokens_reused, ost.tokens_prefilled) == (0, 1 + len(docs), 0, 16 + 194)
+    assert list(eng.store.blocks) == list(oeng.store.blocks)  # identical content keys, identical LRU order
+    assert kl(b, a) < 1e-4
+    reordered = [docs[i] for i in (2, 0, 3, 1)]
+    for ratio, policy in [(0.0, "deviation"), (0.2, "deviation"), (0.5, "deviation"), (1.0, "boundary"),
+                          (0.3, "boundary"), (0.25, "random")]:
+        ga = torch.Generator().manual_seed(123)
+        gb = torch.Generator().manual_seed(123)
+        trace = {}
+        a, cache, st = eng.prefill(on(prefix), on(reordered), on(query), ratio=ratio, policy=policy, gen=ga)
+        b, _, ost = oeng.prefill(prefix, reordered, query, ratio=ratio, policy=policy, gen=gb, trace=trace)
+        assert (st.hits, st.misses, st.tokens_prefilled) == (ost.hits, ost.misses, ost.tokens_prefilled) == \
+               (1 + len(docs), 0, 0)
+        assert st.recompute_eff == pytest.approx(ost.recompute_eff, abs=0)
+        assert cache.length == 16 + 194 + 9
+        assert kl(b, a) < 1e-4, (ratio, policy, kl(b, a))
+        if policy == "deviation" and ratio > 0:
+            S = set(eng.last_selected.cpu().tolist())
+            So = set(trace["S"].tolist())
+            assert len(S) == len(So)
+            dev, all_c = trace["dev"].float(), trace["all_c"]
+            thr = dev.topk(len(So)).values[-1].item()
+            pos_score = {int(p): dev[i].item() for i, p in enumerate(all_c.tolist())}
+            ulp = 2.0 ** (torch.tensor(thr).abs().log2().floor().item() - 7)
+            for p in S ^ So:
+                assert abs(pos_score[p] - thr) <= 2 * ulp, (p, pos_score[p], thr)
+
+
+def test_assembled_cache_layout_is_bit_exact(setup):
+    cfg, gpu, ref = setup
+    m = ref
+    prefix, docs, query = request(cfg, seed=2)
+    eng = Engine(gpu, BlockStore(1 << 30))
+    eng.prefill(on(prefix), on(docs), on(query))
+    reordered = docs[::-1]
+    _, cache, _ = eng.prefill(on(prefix), on(reordered), on(query))
+    pkey = R.block_key(*eng.sig, "", "prefix", prefix)
+    pb = eng.store.blocks[pkey]
+    parts_k, parts_v = [pb.K.cpu()], [pb.V.cpu()]
+    off = len(prefix)
+    for d in reordered:
+        b = eng.store.blocks[R.block_key(*eng.sig, pkey, d)]
+        parts_k.append(R.rotate_keys_fp32(m, b.K.cpu(), off - b.base))
+        parts_v.append(b.V.cpu())
+        off += len(d)
+    T = off
+    K, V = cache.K[..., :T, :].cpu(), cache.V[..., :T, :].cpu()
+    assert torch.equal(V, torch.cat(parts_v, dim=-2))
+    assert torch.equal(K[..., :len(prefix), :], parts_k[0])
+    u = bf16_ulps(K, torch.cat(parts_k, dim=-2))
+    assert u.max().item() <= 1
+
+
+def test_rotation_composes_layer0(setup):
+    """tests/test_engine.py:46-55: layer-0 keys prefilled at 0 and shifted by d equal keys
+    prefilled at +d (only layer 0 is context-free)."""
+    from tread_amd.blend import prefill_kv, rotate_keys
+    cfg, gpu, ref = setup
+    _, docs, _ = request(cfg, seed=3)
+    d = 37
+    K0, _ = prefill_kv(gpu, on(docs[0]))
+    Kd, _ = prefill_kv(gpu, on(torch.cat([torch.zeros(d, dtype=torch.long), docs[0]])))
+    a, b = rotate_keys(gpu, K0[0], d).float(), Kd[0][:, :, d:].float()
+    assert (a - b).abs().max().item() < 0.05 * b.abs().max().item()
+
+
+def test_full_recompute_matches_full_prefill(setup):
+    """tests/test_engine.py:58-65: ratio=1.0 (boundary) reproduces full prefill."""
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=4)
+    eng = Engine(gpu, BlockStore(1 << 30))
+    full, _, _ = prefill_full(gpu, on(prefix), on(docs), on(query))
+    out, _, _ = eng.prefill(on(prefix), on(docs), on(query), ratio=1.0, policy="boundary")
+    oref, _, _ = R.prefill_full(ref, prefix, docs, query)
+    assert kl(full, out) < 1e-4
+    assert kl(oref, full) < 1e-4
+
+
+def test_prefix_only_matches_full_prefill(setup):
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=5)
+    eng = Engine(gpu, BlockStore(1 << 30))
+    full, _, _ = prefill_full(gpu, on(prefix), on(docs), on(query))
+    out, _, st = eng.prefill_prefix_only(on(prefix), on(docs), on(query))
+    assert kl(full, out) < 1e-4
+    assert st.tokens_prefilled == sum(len(d) for d in docs) + len(prefix)
+
+
+def test_reordered_request_hits_and_matches_cold_assembly(setup):
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=6)
+    eng = Engine(gpu, BlockStore(1 << 30))
+    _, _, st1 = eng.prefill(on(prefix), on(docs), on(query))
+    assert st1.hits == 0 and st1.misses == 1 + len(docs)
+    reordered = docs[::-1]
+    warm, _, st2 = eng.prefill(on(prefix), on(reordered), on(query))
+    assert st2.hits == 1 + len(docs) and st2.misses == 0 and st2.tokens_prefilled == 0
+    cold, _, _ = Engine(gpu, BlockStore(1 << 30)).prefill(on(prefix), on(reordered), on(query))
+    assert kl(cold, warm) < 1e-4
+
+
+def test_packed_cold_path_matches_per_doc_prefill(setup):
+    """tests/test_engine.py:116-129: packed miss prefill == each doc prefilled after the prefix."""
+    from tread_amd.blend import assemble
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=7)
+    K_ref, V_ref = assemble(gpu, on(prefix), on(docs), "shared")
+    eng = Engine(gpu, BlockStore(1 << 30))
+    out, cache, st = eng.prefill(on(prefix), on(docs), on(query))
+    assert st.misses == 1 + len(docs)
+    T = len(prefix) + sum(len(d) for d in docs)
+    for l in (0, len(K_ref) // 2, len(K_ref) - 1):
+        a, b = cache.key_cache[l][:, :, :T].float(), K_ref[l].float()
+        assert (a - b).abs().max().item() < 0.05 * b.abs().max().item()
+    # against the oracle's per-doc assembly too
+    oK, oV = R.assemble(ref, prefix, docs, "shared")
+    orf = M.logits_last(ref, M.forward(ref, query, past=(oK, oV))[0])
+    assert kl(orf, out) < 1e-4
+
+
+def test_cpu_tier_offloads_and_serves_hits(setup):
+    """tests/test_engine.py:132-148 with the async pinned tier."""
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=8)
+    probe = BlockStore(1 << 30)
+    Engine(gpu, probe).prefill(on(prefix), on(docs), on(query))
+    one_block = max(b.nbytes for b in probe.blocks.values())
+    store = BlockStore(2 * one_block, cpu_budget_bytes=1 << 30)
+    eng = Engine(gpu, store)
+    eng.prefill(on(prefix), on(docs), on(query))
+    assert store.stats.offloads > 0 and store.stats.bytes_used <= store.budget
+    assert store.stats.cpu_evictions == 0
+    for b in store.cpu_blocks.values():
+        b.synchronize()
+        assert not b.K.is_cuda and b.K.is_pinned()
+    warm, _, st = eng.prefill(on(prefix), on(docs[::-1]), on(query))
+    assert st.misses == 0 and store.stats.cpu_hits > 0
+    cold, _, _ = Engine(gpu, BlockStore(1 << 30)).prefill(on(prefix), on(docs[::-1]), on(query))
+    assert kl(cold, warm) < 1e-4
+    # same stats trace as the oracle store under the same request sequence
+    ostore = R.BlockStore(2 * one_block, cpu_budget_bytes=1 << 30)
+    oeng = R.Engine(ref, ostore)
+    oeng.prefill(prefix, docs, query)
+    oeng.prefill(prefix, docs[::-1], query)
+    assert vars(store.stats) == vars(ostore.stats)
+    assert list(store.blocks) == list(ostore.blocks) and list(store.cpu_blocks) == list(ostore.cpu_blocks)
+
+
+def test_block_key_depends_on_prefix(setup):
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=9)
+    eng = Engine(gpu, BlockStore(1 << 30))
+    eng.prefill(on(prefix), on(docs), on(query))
+    other = (prefix + 1) % cfg.vocab_size
+    _, _, st = eng.prefill(on(other), on(docs), on(query))
+    assert st.hits == 0
+
+
+def test_eviction_respects_budget(setup):
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=10)
+    store = BlockStore(1 << 30)
+    Engine(gpu, store).prefill(on(prefix), on(docs), on(query))
+    one_block = max(b.nbytes for b in store.blocks.values())
+    small = BlockStore(2 * one_block)
+    eng = Engine(gpu, small)
+    eng.prefill(on(prefix), on(docs), on(query))
+    assert small.stats.bytes_used <= small.budget and small.stats.evictions > 0
+    full, _, _ = prefill_full(gpu, on(prefix), on(docs), on(query))
+    out, _, _ = eng.prefill(on(prefix), on(docs), on(query), ratio=1.0, policy="boundary")
+    assert kl(full, out) < 1e-4
+
+
+@pytest.mark.parametrize("policy,ratio", [("deviation", 0.2), ("boundary", 0.3), ("boundary", 1.0)])
+def test_graph_blend_matches_eager(setup, policy, ratio):
+    """tests/test_engine.py:95-113: the hipGraph replay equals the eager loop; one capture."""
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=11)
+    eager = Engine(gpu, BlockStore(1 << 30))
+    graphed = Engine(gpu, BlockStore(1 << 30), graphs=True)
+    eager.prefill(on(prefix), on(docs), on(query))
+    graphed.prefill(on(prefix), on(docs), on(query))
+    a, _, _ = eager.prefill(on(prefix), on(docs[::-1]), on(query), ratio=ratio, policy=policy)
+    for _ in range(3):  # replays after the first must agree too
+        b, _, _ = graphed.prefill(on(prefix), on(docs[::-1]), on(query), ratio=ratio, policy=policy)
+        assert kl(a, b) < 1e-4
+        torch.cuda.synchronize()
+    assert graphed.runner.captures == 1
+    if ratio == 1.0:
+        full, _, _ = prefill_full(gpu, on(prefix), on(docs[::-1]), on(query))
+        assert kl(full, b) < 1e-4
+
+
+def test_empty_docs_and_zero_budget(setup):
+    cfg, gpu, ref = setup
+    prefix, _, query = request(cfg, seed=12)
+    eng = Engine(gpu, BlockStore(1 << 30))
+    out, cache, st = eng.prefill(on(prefix), [], on(query), ratio=0.5)
+    full, _, _ = prefill_full(gpu, on(prefix), [], on(query))
+    assert kl(full, out) < 1e-4 and st.recompute_eff == 0.0
+    _, docs, _ = request(cfg, seed=12, n_docs=1, lens=(3,))
+    _, _, st = eng.prefill(on(prefix), on(docs), on(query), ratio=0.1)  # round(0.3) == 0
+    assert st.recompute_eff == 0.0

@@ -1,0 +1,286 @@
+"""Kernel-level parity of libtread_hip.so against the CPU oracle (and fp32 textbook formulas).
+
+Every test builds seeded inputs on the CPU, runs the HIP kernel through tread_amd._hip (the C-ABI)
+and compares with the oracle's restatement of the reference op on the same inputs.
+"""
+import pytest
+import torch
+
+from oracle import model_ref as M
+from oracle import tread_ref as R
+from tread_amd import _hip
+from tread_amd.model import ModelConfig
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def bf16_ulps(a, b):
+    """Distance in bf16 units in the last place between two bf16 tensors (same shape)."""
+    def ordered(t):
+        i = t.contiguous().view(torch.int16).to(torch.int32)
+        return torch.where(i >= 0, i, -(i + 32768))
+    return (ordered(a.cpu()) - ordered(b.cpu())).abs()
+
+
+def _cfg(hd, theta=1000000.0):
+    return ModelConfig(64, 64, 2, 2, 1, hd, 64, rope_theta=theta)
+
+
+def _ref_model(hd, theta=1000000.0):
+    cfg = _cfg(hd, theta)
+    return M.RefModel(cfg=cfg, w={}, dtype=torch.bfloat16, inv_freq=M.inv_freq_of(cfg))
+
+
+# ------------------------------------------------------------------------------------------- (a)
+
+@pytest.mark.parametrize("hd,kv,L", [(128, 4, 3), (64, 2, 2)])
+def test_rope_assemble_matches_fp32_rotation_and_cat_layout(hd, kv, L):
+    g = torch.Generator().manual_seed(11)
+    m = _ref_model(hd)
+    P = 64
+    lens = [1, 127, 128, 129, 300, 1000]
+    t_cap = P + sum(lens) + 40
+    prefK = torch.randn(L, 1, kv, P, hd, generator=g).to(torch.bfloat16)
+    prefV = torch.randn(L, 1, kv, P, hd, generator=g).to(torch.bfloat16)
+    srcs, exp_K, exp_V, exp_Kbf = [(prefK, prefV, 0, 0)], [prefK], [prefV], [prefK]
+    off = P
+    for i, n in enumerate(lens):
+        K = (3 * torch.randn(L, 1, kv, n, hd, generator=g)).to(torch.bfloat16)
+        V = torch.randn(L, 1, kv, n, hd, generator=g).to(torch.bfloat16)
+        delta = off - P if i != 2 else -(i + 5)  # one negative shift for generality
+        srcs.append((K, V, off, delta))
+        exp_K.append(R.rotate_keys_fp32(m, K, delta))
+        exp_Kbf.append(R.rotate_keys(m, K, delta))
+        exp_V.append(V)
+        off += n
+    T = off
+    sentinel = torch.tensor(-7.0, dtype=torch.bfloat16)
+    dK = torch.full((L, 1, kv, t_cap, hd), -7.0, dtype=torch.bfloat16, device=DEV)
+    dV = torch.full_like(dK, -7.0)
+    dsrcs = [(K.to(DEV), V.to(DEV), o, d) for K, V, o, d in srcs]
+    _hip.rope_assemble(dsrcs, dK, dV, m.inv_freq)
+    torch.cuda.synchronize()
+    gK, gV = dK.cpu(), dV.cpu()
+    eK, eV = torch.cat(exp_K, dim=-2), torch.cat(exp_V, dim=-2)
+    # V and the delta-0 prefix: bit copies; layout equals torch.cat
+    assert torch.equal(gV[..., :T, :], eV)
+    assert torch.equal(gK[..., :P, :], prefK)
+    # K: within 1 bf16 ulp of the fp32 reference rotation
+    u = bf16_ulps(gK[..., :T, :], eK)
+    assert u.max().item() <= 1, u.max()
+    assert (u == 0).float().mean().item() > 0.99
+    # rows past T untouched
+    assert (gK[..., T:, :] == sentinel).all() and (gV[..., T:, :] == sentinel).all()
+    # distance to the reference's own bf16 torch path (cos/sin rounded to bf16): reported bound
+    ub = bf16_ulps(gK[..., :T, :], torch.cat(exp_Kbf, dim=-2))
+    assert ub.float().mean().item() < 4
+
+
+def test_rope_assemble_layer_range_and_rejects_bad_rows():
+    m = _ref_model(128)
+    L, kv, hd, n = 4, 2, 128, 50
+    K = torch.randn(L, 1, kv, n, hd).to(torch.bfloat16).to(DEV)
+    V = torch.randn(L, 1, kv, n, hd).to(torch.bfloat16).to(DEV)
+    dK = torch.zeros(L, 1, kv, 80, hd, dtype=torch.bfloat16, device=DEV)
+    dV = torch.zeros_like(dK)
+    _hip.rope_assemble([(K, V, 10, 5)], dK, dV, m.inv_freq, layer_lo=1, layer_hi=3)
+    torch.cuda.synchronize()
+    assert (dV[0] == 0).all() and (dV[3] == 0).all()
+    assert torch.equal(dV[1:3, :, :, 10:60].cpu(), V[1:3].cpu())
+    with pytest.raises(RuntimeError, match="outside the cache"):
+        _hip.rope_assemble([(K, V, 40, 0)], dK, dV, m.inv_freq)
+
+
+# ------------------------------------------------------------------------------------ RoPE / glue
+
+@pytest.mark.parametrize("hd,theta", [(128, 1000000.0), (64, 10000.0), (128, 500000.0)])
+def test_rope_table_matches_reference_rotary_emb(hd, theta):
+    m = _ref_model(hd, theta)
+    pos = torch.cat([torch.arange(0, 70), torch.randint(0, 40000, (500,), generator=torch.Generator().manual_seed(1))])
+    cos, sin = _hip.rope_table(pos.to(DEV), m.inv_freq, hd)
+    rc, rs = M.rope_cos_sin(m, pos, torch.bfloat16)  # [1, n, hd]
+    for got, ref in ((cos, rc[0, :, :hd // 2]), (sin, rs[0, :, :hd // 2])):
+        u = bf16_ulps(got, ref)
+        assert u.max().item() <= 1
+        assert (u == 0).float().mean().item() > 0.995
+
+
+@pytest.mark.parametrize("hd,hq,hkv", [(128, 7, 1), (64, 14, 2), (128, 8, 8)])
+def test_qkv_rope_splice_bit_exact_vs_apply_rotary(hd, hq, hkv):
+    g = torch.Generator().manual_seed(5)
+    m = _ref_model(hd)
+    n, t_cap = 37, 200
+    qkv = torch.randn(n, (hq + 2 * hkv) * hd, generator=g).to(torch.bfloat16)
+    rows = torch.randperm(t_cap, generator=g)[:n]
+    pos = torch.randint(0, 33000, (n,), generator=g)
+    cos, sin = M.rope_cos_sin(m, pos, torch.bfloat16)
+    Kc = torch.zeros(1, hkv, t_cap, hd, dtype=torch.bfloat16, device=DEV)
+    Vc = torch.zeros_like(Kc)
+    q_out = torch.empty(n, hq, hd, dtype=torch.bfloat16, device=DEV)
+    _hip.qkv_rope_splice(qkv.to(DEV), cos[0, :, :hd // 2].contiguous().to(DEV), sin[0, :, :hd // 2].contiguous().to(DEV),
+                         rows.to(DEV), hq, hkv, hd, Kc, Vc, q_out=q_out)
+    torch.cuda.synchronize()
+    q = qkv[:, :hq * hd].view(1, n, hq, hd).transpose(1, 2)
+    k = qkv[:, hq * hd:(hq + hkv) * hd].view(1, n, hkv, hd).transpose(1, 2)
+    v = qkv[:, (hq + hkv) * hd:].view(1, n, hkv, hd).transpose(1, 2)
+    qr, kr = M.apply_rope(q, cos, sin), M.apply_rope(k, cos, sin)
+    assert torch.equal(q_out.cpu(), qr[0].transpose(0, 1))
+    assert torch.equal(Kc.cpu()[0][:, rows], kr[0])
+    assert torch.equal(Vc.cpu()[0][:, rows], v[0])
+    mask = torch.ones(t_cap, dtype=torch.bool)
+    mask[rows] = False
+    assert (Kc.cpu()[0][:, mask] == 0).all()
+
+
+@pytest.mark.parametrize("H", [896, 1536, 3584, 8192])
+def test_add_rmsnorm_vs_hf_rmsnorm(H):
+    g = torch.Generator().manual_seed(2)
+    n = 33
+    x = torch.randn(n, H, generator=g).to(torch.bfloat16)
+    d = torch.randn(n, H, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    s, y = _hip.add_rmsnorm(x.to(DEV), w.to(DEV), 1e-6, delta=d.to(DEV))
+    rs = x + d
+    ry = M.rms_norm(rs, w, 1e-6)
+    assert torch.equal(s.cpu(), rs)
+    u = bf16_ulps(y, ry)
+    assert u.max().item() <= 1 and (u == 0).float().mean().item() > 0.99
+    _, y2 = _hip.add_rmsnorm(x.to(DEV), w.to(DEV), 1e-6)
+    assert bf16_ulps(y2, M.rms_norm(x, w, 1e-6)).max().item() <= 1
+
+
+def test_silu_mul_vs_torch():
+    g = torch.Generator().manual_seed(3)
+    n, I = 19, 4864
+    gu = (2 * torch.randn(n, 2 * I, generator=g)).to(torch.bfloat16)
+    out = _hip.silu_mul(gu.to(DEV))
+    ref = torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]
+    u = bf16_ulps(out, ref)
+    assert u.max().item() <= 1 and (u == 0).float().mean().item() > 0.99
+
+
+# ------------------------------------------------------------------------------------------- (b)
+
+@pytest.mark.parametrize("hd,hkv", [(128, 4), (64, 2), (128, 8)])
+def test_dev_score_matches_reference_expression(hd, hkv):
+    g = torch.Generator().manual_seed(7)
+    m = _ref_model(hd)
+    n, t_cap = 301, 1200
+    kv_raw = torch.randn(n, 2 * hkv * hd, generator=g).to(torch.bfloat16)
+    rows = torch.sort(torch.randperm(t_cap, generator=g)[:n]).values
+    K1 = torch.randn(1, hkv, t_cap, hd, generator=g).to(torch.bfloat16)
+    V1 = torch.randn(1, hkv, t_cap, hd, generator=g).to(torch.bfloat16)
+    cos, sin = M.rope_cos_sin(m, rows, torch.bfloat16)
+    # make some candidates drift little: copy the cache row (planted near-ties / zeros)
+    k = kv_raw[:, :hkv * hd].view(1, n, hkv, hd).transpose(1, 2)
+    v = kv_raw[:, hkv * hd:].view(1, n, hkv, hd).transpose(1, 2)
+    k1 = M.apply_rope(k, cos, sin)
+    ref = R.deviation_score(k1, v, K1[:, :, rows], V1[:, :, rows])[0]
+    got = _hip.dev_score(kv_raw.to(DEV), cos[0, :, :hd // 2].contiguous().to(DEV),
+                         sin[0, :, :hd // 2].contiguous().to(DEV), rows.to(DEV), hkv, hd, K1.to(DEV), V1.to(DEV))
+    u = bf16_ulps(got, ref)
+    assert u.max().item() <= 1
+    assert (u == 0).float().mean().item() > 0.98
+
+
+def _brute_topk(score, k):
+    s = score.float().tolist()
+    order = sorted(range(len(s)), key=lambda i: (-s[i], i))
+    return sorted(order[:k])
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (10, 0), (10, 10), (1000, 200), (32000, 6400), (32000, 16000), (40000, 1)])
+def test_topk_select_equals_brute_force(n, k):
+    g = torch.Generator().manual_seed(n + k)
+    # few distinct bf16 values => many ties at the threshold
+    score = (torch.randint(0, 50, (n,), generator=g).float() / 8 + 3).to(torch.bfloat16)
+    sel = _hip.topk_select(score.to(DEV), k).cpu().tolist()
+    assert sel == _brute_topk(score, k)
+    if k:
+        # same as torch.topk up to the tie order at the threshold
+        thr = score.float().topk(k).values[-1]
+        ref = set(score.float().topk(k).indices.tolist())
+        got = set(sel)
+        assert all(score[i].float() == thr for i in got ^ ref)
+
+
+def test_topk_select_handles_negative_and_distinct_scores():
+    g = torch.Generator().manual_seed(9)
+    score = torch.randn(5000, generator=g).to(torch.bfloat16)
+    sel = _hip.topk_select(score.to(DEV), 777).cpu().tolist()
+    assert sel == _brute_topk(score, 777)
+
+
+# ------------------------------------------------------------------------------------------- (c)
+
+def ref_attention(q, K, V, kend, scale, kseg=None, n_shared=0):
+    """Textbook masked GQA softmax attention in fp32 on the CPU. q [n, hq, hd], K/V [hkv, T, hd]."""
+    n, hq, hd = q.shape
+    hkv, T, _ = K.shape
+    G = hq // hkv
+    Kf = K.float().repeat_interleave(G, 0)
+    Vf = V.float().repeat_interleave(G, 0)
+    s = torch.einsum("nhd,htd->nht", q.float(), Kf) * scale
+    keys = torch.arange(T)
+    vis = keys[None, :] <= kend[:, None]
+    if kseg is not None:
+        vis &= (keys[None, :] < n_shared) | (keys[None, :] >= kseg[:, None])
+    s = s.masked_fill(~vis[:, None, :], float("-inf"))
+    return torch.einsum("nht,htd->nhd", torch.softmax(s, -1), Vf)
+
+
+CASES = [
+    # hq, hkv, hd, t_cap, n, kind
+    (8, 2, 128, 700, 137, "subset"),
+    (14, 2, 64, 1030, 300, "subset"),
+    (28, 4, 128, 2100, 1, "subset"),
+    (28, 4, 128, 3000, 600, "subset"),
+    (12, 2, 128, 513, 513, "prefill"),
+    (7, 1, 64, 200, 64, "prefill"),
+    (6, 3, 64, 900, 250, "subset"),
+    (64, 8, 128, 1500, 90, "subset"),
+    (8, 2, 128, 700, 337, "segments"),
+    (14, 2, 64, 500, 230, "segments"),
+]
+
+
+@pytest.mark.parametrize("hq,hkv,hd,t_cap,n,kind", CASES)
+def test_subset_attention_vs_textbook(hq, hkv, hd, t_cap, n, kind):
+    g = torch.Generator().manual_seed(hq * 1000 + n)
+    q = torch.randn(n, hq, hd, generator=g).to(torch.bfloat16)
+    K = torch.randn(hkv, t_cap, hd, generator=g).to(torch.bfloat16)
+    V = torch.randn(hkv, t_cap, hd, generator=g).to(torch.bfloat16)
+    kseg, n_shared = None, 0
+    if kind == "subset":
+        kend = torch.sort(torch.randperm(t_cap, generator=g)[:n]).values
+    elif kind == "prefill":
+        kend = torch.arange(n)
+    else:  # packed docs on a shared prefix: block-diagonal visibility
+        n_shared = 40
+        lens = [100, 37, n - 137]
+        kend = n_shared + torch.arange(n)
+        kseg = torch.cat([torch.full((Ld,), n_shared + o) for Ld, o in zip(lens, [0, 100, 137])])
+    scale = hd ** -0.5
+    ref = ref_attention(q, K, V, kend, scale, kseg, n_shared)
+    out = _hip.subset_attn(q.to(DEV), K.to(DEV), V.to(DEV), kend.to(DEV), hq, hkv, hd, scale,
+                           kseg=None if kseg is None else kseg.to(DEV), n_shared=n_shared)
+    got = out.cpu().float().view(n, hq, hd)
+    err = (got - ref).abs()
+    assert err.max().item() < 3e-2, err.max()
+    assert err.mean().item() < 3e-3, err.mean()
+
+
+# ------------------------------------------------------------------------------------------- (d)
+
+def test_copy_async_roundtrip_pinned():
+    s = torch.cuda.Stream()
+    src = torch.randn(3, 1000, 77).to(torch.bfloat16).pin_memory()
+    dev = torch.empty(src.shape, dtype=src.dtype, device=DEV)
+    back = torch.empty(src.shape, dtype=src.dtype).pin_memory()
+    e1, e2 = torch.cuda.Event(), torch.cuda.Event()
+    _hip.copy_async(dev, src, s, e1)
+    s.wait_event(e1)
+    _hip.copy_async(back, dev, s, e2)
+    e2.synchronize()
+    assert torch.equal(back, src)

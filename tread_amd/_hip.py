@@ -1,0 +1,247 @@
+"""ctypes binding of libtread_hip.so (include/tread_hip.h) and torch-facing wrappers.
+
+The wrappers validate shapes, dtypes, devices and contiguity on the host, then pass raw device
+pointers and torch's current HIP stream to the C entry points. There is no fallback: if the
+library is missing or a call fails, a RuntimeError says why.
+"""
+import ctypes
+from pathlib import Path
+
+import torch  # loads torch's HIP runtime first, so the library below binds to the same one
+
+LIB_PATH = Path(__file__).resolve().with_name("libtread_hip.so")
+ABI_VERSION = 1
+
+c_i64, c_int, c_void, c_float, c_size = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
+P_I64 = ctypes.POINTER(ctypes.c_int64)
+P_F32 = ctypes.POINTER(ctypes.c_float)
+
+
+class Src(ctypes.Structure):
+    """tread_src_t."""
+    _fields_ = [("k", c_void), ("v", c_void), ("n_tokens", c_i64), ("dst_off", c_i64), ("delta", c_i64)]
+
+
+_SIGS = {
+    "tread_last_error": (ctypes.c_char_p, []),
+    "tread_abi_version": (c_int, []),
+    "tread_rope_assemble_bf16": (c_int, [ctypes.POINTER(Src), c_int, c_void, c_void, c_int, c_int, c_i64, c_int,
+                                         P_F32, c_int, c_int, c_void]),
+    "tread_rope_table_bf16": (c_int, [c_void, c_i64, P_F32, c_int, c_void, c_void, c_void]),
+    "tread_qkv_rope_splice_bf16": (c_int, [c_void, c_void, c_void, c_i64, c_void, c_void, c_void, c_i64, c_int,
+                                           c_int, c_int, c_void, c_void, c_void, c_i64, c_void]),
+    "tread_dev_score_bf16": (c_int, [c_void, c_void, c_i64, c_void, c_void, c_void, c_i64, c_int, c_int, c_void,
+                                     c_void, c_i64, c_void, c_void]),
+    "tread_topk_workspace_bytes": (c_size, [c_i64]),
+    "tread_topk_select_bf16": (c_int, [c_void, c_i64, c_i64, c_void, c_void, c_size, c_void]),
+    "tread_subset_attn_bf16": (c_int, [c_void, c_void, c_void, c_void, c_void, c_i64, c_i64, c_int, c_int, c_int,
+                                       c_i64, c_float, c_void, c_void]),
+    "tread_add_rmsnorm_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_int, c_void, c_void, c_void]),
+    "tread_silu_mul_bf16": (c_int, [c_void, c_i64, c_int, c_void, c_void]),
+    "tread_copy_async": (c_int, [c_void, c_void, c_size, c_void, c_void]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load the library once; raise if it is missing (no CPU fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python -m tread_amd.csrc.build` "
+                               "(or __graft_entry__.build()) first")
+        l = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            f = getattr(l, name)
+            f.restype, f.argtypes = res, args
+        if l.tread_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH}: ABI {l.tread_abi_version()} != {ABI_VERSION}; rebuild it")
+        _lib = l
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+def _check(name, rc):
+    if rc != 0:
+        msg = lib().tread_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need(t, name, dtype=torch.bfloat16, contig=True):
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (the HIP path has no CPU fallback)")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if contig and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _freq(inv_freq):
+    f = inv_freq.detach().to("cpu", torch.float32).contiguous()
+    return f, ctypes.cast(f.data_ptr(), P_F32)
+
+
+# ------------------------------------------------------------------------------------------- (a)
+
+def rope_assemble(sources, dst_k, dst_v, inv_freq, layer_lo=0, layer_hi=None):
+    """sources: list of (K, V, dst_off, delta) with K, V [L, 1, kv, n, hd] bf16 on the GPU.
+    dst_k, dst_v: [L, 1, kv, t_cap, hd]. Rotates K by delta (fp32 cos/sin), copies V."""
+    _need(dst_k, "dst_k")
+    _need(dst_v, "dst_v")
+    L, one, kv, t_cap, hd = dst_k.shape
+    if dst_v.shape != dst_k.shape or one != 1:
+        raise ValueError("dst_k / dst_v must both be [L, 1, kv, t_cap, hd]")
+    layer_hi = L if layer_hi is None else layer_hi
+    arr = (Src * max(1, len(sources)))()
+    for i, (K, V, off, delta) in enumerate(sources):
+        _need(K, f"source {i} K")
+        _need(V, f"source {i} V")
+        if K.shape[:3] != (L, 1, kv) or K.shape[-1] != hd or V.shape != K.shape:
+            raise ValueError(f"source {i}: shape {tuple(K.shape)} does not match cache {tuple(dst_k.shape)}")
+        arr[i] = Src(K.data_ptr(), V.data_ptr(), K.shape[-2], int(off), int(delta))
+    f, fp = _freq(inv_freq)
+    _check("tread_rope_assemble_bf16", lib().tread_rope_assemble_bf16(
+        arr, len(sources), _ptr(dst_k), _ptr(dst_v), L, kv, t_cap, hd, fp, layer_lo, layer_hi, _stream()))
+
+
+# ------------------------------------------------------------------------------------ RoPE / glue
+
+def rope_table(pos, inv_freq, head_dim):
+    """bf16 cos, sin [n, head_dim/2] for int64 positions, rounded like the reference's rotary_emb."""
+    _need(pos, "pos", torch.int64)
+    n = pos.numel()
+    cos = torch.empty(n, head_dim // 2, dtype=torch.bfloat16, device=pos.device)
+    sin = torch.empty_like(cos)
+    f, fp = _freq(inv_freq)
+    _check("tread_rope_table_bf16", lib().tread_rope_table_bf16(_ptr(pos), n, fp, head_dim, _ptr(cos), _ptr(sin),
+                                                               _stream()))
+    return cos, sin
+
+
+def qkv_rope_splice(qkv, cos, sin, rows, hq, hkv, hd, k_cache, v_cache, q_out=None, q_col=0, k_col=None, v_col=None):
+    """qkv: [n, ld] GEMM output holding q at column q_col, k at k_col, v at v_col (defaults: q|k|v).
+    k_cache / v_cache: one layer [1, hkv, t_cap, hd] (or [hkv, t_cap, hd]). q_out: [n, hq, hd] or None."""
+    _need(qkv, "qkv")
+    _need(rows, "rows", torch.int64)
+    _need(k_cache, "k_cache")
+    _need(v_cache, "v_cache")
+    n, ld = qkv.shape
+    k_col = hq * hd if k_col is None else k_col
+    v_col = k_col + hkv * hd if v_col is None else v_col
+    t_cap = k_cache.shape[-2]
+    if k_cache.shape[-3] != hkv or k_cache.shape[-1] != hd or v_cache.shape != k_cache.shape:
+        raise ValueError("cache shape mismatch")
+    if q_out is not None:
+        _need(q_out, "q_out")
+        if q_out.numel() != n * hq * hd:
+            raise ValueError("q_out shape mismatch")
+    base = qkv.data_ptr()
+    es = qkv.element_size()
+    _check("tread_qkv_rope_splice_bf16", lib().tread_qkv_rope_splice_bf16(
+        ctypes.c_void_p(base + q_col * es), ctypes.c_void_p(base + k_col * es), ctypes.c_void_p(base + v_col * es),
+        ld, _ptr(cos), _ptr(sin), _ptr(rows), n, hq, hkv, hd, _ptr(q_out), _ptr(k_cache), _ptr(v_cache), t_cap,
+        _stream()))
+
+
+def add_rmsnorm(x, weight, eps, delta=None, sum_out=None, norm_out=None):
+    """norm_out = weight * bf16(s * rsqrt(mean(s^2) + eps)), s = x + delta (bf16). Returns (s, norm)."""
+    _need(x, "x")
+    _need(weight, "weight")
+    H = x.shape[-1]
+    n = x.numel() // H
+    if delta is not None:
+        _need(delta, "delta")
+        if sum_out is None:
+            sum_out = torch.empty_like(x)
+    if norm_out is None:
+        norm_out = torch.empty_like(x)
+    _check("tread_add_rmsnorm_bf16", lib().tread_add_rmsnorm_bf16(
+        _ptr(x), _ptr(delta), _ptr(weight), float(eps), n, H, _ptr(sum_out), _ptr(norm_out), _stream()))
+    return (sum_out if delta is not None else x), norm_out
+
+
+def silu_mul(gate_up, out=None):
+    _need(gate_up, "gate_up")
+    two_i = gate_up.shape[-1]
+    n = gate_up.numel() // two_i
+    if out is None:
+        out = torch.empty(*gate_up.shape[:-1], two_i // 2, dtype=gate_up.dtype, device=gate_up.device)
+    _check("tread_silu_mul_bf16", lib().tread_silu_mul_bf16(_ptr(gate_up), n, two_i // 2, _ptr(out), _stream()))
+    return out
+
+
+# ------------------------------------------------------------------------------------------- (b)
+
+def dev_score(kv, cos, sin, rows, hkv, hd, k_cache, v_cache, k_col=0, v_col=None, out=None):
+    """kv: [n, ld] with raw (bias added, pre-RoPE) k at k_col and v at v_col. Returns bf16 [n]."""
+    _need(kv, "kv")
+    _need(rows, "rows", torch.int64)
+    _need(k_cache, "k_cache")
+    _need(v_cache, "v_cache")
+    n, ld = kv.shape
+    v_col = k_col + hkv * hd if v_col is None else v_col
+    if out is None:
+        out = torch.empty(n, dtype=torch.bfloat16, device=kv.device)
+    es = kv.element_size()
+    _check("tread_dev_score_bf16", lib().tread_dev_score_bf16(
+        ctypes.c_void_p(kv.data_ptr() + k_col * es), ctypes.c_void_p(kv.data_ptr() + v_col * es), ld, _ptr(cos),
+        _ptr(sin), _ptr(rows), n, hkv, hd, _ptr(k_cache), _ptr(v_cache), k_cache.shape[-2], _ptr(out), _stream()))
+    return out
+
+
+def topk_select(score, k, out=None):
+    """Indices of the k largest bf16 scores, ascending; ties at the threshold go to the lowest indices."""
+    _need(score, "score")
+    n = score.numel()
+    if out is None:
+        out = torch.empty(k, dtype=torch.int64, device=score.device)
+    _check("tread_topk_select_bf16", lib().tread_topk_select_bf16(_ptr(score), n, k, _ptr(out), None, 0, _stream()))
+    return out
+
+
+# ------------------------------------------------------------------------------------------- (c)
+
+def subset_attn(q, k_cache, v_cache, kend, hq, hkv, hd, scale, kseg=None, n_shared=0, out=None):
+    """q: [n, hq, hd]; k_cache/v_cache: one layer [(1,) hkv, t_cap, hd]; kend/kseg: int64 [n].
+    Returns out [n, hq*hd]."""
+    _need(q, "q")
+    _need(k_cache, "k_cache")
+    _need(v_cache, "v_cache")
+    _need(kend, "kend", torch.int64)
+    if kseg is not None:
+        _need(kseg, "kseg", torch.int64)
+    n = kend.numel()
+    if q.numel() != n * hq * hd:
+        raise ValueError(f"q has {q.numel()} elements, expected {n}x{hq}x{hd}")
+    if out is None:
+        out = torch.empty(n, hq * hd, dtype=q.dtype, device=q.device)
+    _check("tread_subset_attn_bf16", lib().tread_subset_attn_bf16(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(kend), _ptr(kseg), int(n_shared), n, hq, hkv, hd,
+        k_cache.shape[-2], float(scale), _ptr(out), _stream()))
+    return out
+
+
+# ------------------------------------------------------------------------------------------- (d)
+
+def copy_async(dst, src, stream, event=None):
+    """DMA src -> dst (pinned host <-> device) on `stream` (a torch.cuda.Stream); records `event`."""
+    if dst.numel() * dst.element_size() != src.numel() * src.element_size():
+        raise ValueError("copy_async: size mismatch")
+    if not (dst.is_contiguous() and src.is_contiguous()):
+        raise ValueError("copy_async: tensors must be contiguous")
+    _check("tread_copy_async", lib().tread_copy_async(
+        _ptr(dst), _ptr(src), src.numel() * src.element_size(), ctypes.c_void_p(stream.cuda_stream), None))
+    if event is not None:
+        event.record(stream)  # torch events are created lazily on first record

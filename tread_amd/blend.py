@@ -1,0 +1,212 @@
+"""KV ops of the reuse path: re-rotation, assembly, deviation scoring and selective recompute.
+
+Public names and signatures follow tread/blend.py (prefill_kv, rotate_keys, chunk_kv, assemble,
+_subset_ctx, _qkv, _layer_subset, layer1_deviation, blend, to_cache) so callers written against
+the reference keep working. KV tensors are [1, kv_heads, T, head_dim] per layer (post-RoPE keys),
+blocks are stacked [L, 1, kv_heads, n, head_dim]. All arithmetic runs in the HIP kernels of
+libtread_hip.so (tread_amd._hip) plus torch GEMMs; bf16 on the GPU only.
+"""
+import weakref
+
+import torch
+import torch.nn.functional as F
+
+from tread_amd import _hip
+from tread_amd.cache import KVCache
+from tread_amd.forward import alloc_cache, embed, final_logits, make_rows, run_layers, layer_forward
+from tread_amd.model import prepare
+
+_PREPARED = weakref.WeakKeyDictionary()
+
+
+def prepared(model):
+    """Fused-weight view of `model` (built once per model object)."""
+    P = _PREPARED.get(model)
+    if P is None:
+        if model.dtype != torch.bfloat16:
+            raise TypeError(f"the HIP path computes in bf16; model dtype is {model.dtype}")
+        P = prepare(model)
+        _PREPARED[model] = P
+    return P
+
+
+def forward_into(model, ids, K, V, start_row=0, pos=None, kseg=None, n_shared=0, want_logits=True):
+    """Forward `ids` whose k/v land in cache rows start_row.. of K, V ([L, 1, kv, t_cap, hd]),
+    attending causally to every earlier row (or block-diagonally with kseg / n_shared)."""
+    P = prepared(model)
+    n = len(ids)
+    rows = torch.arange(start_row, start_row + n, device=ids.device)
+    R = make_rows(P, rows, pos=pos, kseg=kseg, n_shared=n_shared)
+    Kl, Vl = K.unbind(0), V.unbind(0)
+    h, d = run_layers(P, embed(P, ids), None, R, Kl, Vl, range(P.L))
+    return final_logits(P, h, d) if want_logits else None
+
+
+def prefill_kv(model, ids):
+    """tread/blend.py:12-19: per-layer (K, V) lists of a forward over `ids` from position 0."""
+    P = prepared(model)
+    K, V = alloc_cache(P, len(ids), ids.device)
+    forward_into(model, ids, K, V, want_logits=False)
+    return list(K.unbind(0)), list(V.unbind(0))
+
+
+def rotate_keys(model, K, delta):
+    """tread/blend.py:22-39: shift post-RoPE keys by `delta` positions, R(p + delta) = R(delta) R(p).
+
+    delta 0 returns K itself. Otherwise one pass of the fused re-rotation kernel with fp32
+    cos/sin and one rounding to bf16 (the fp32-reference result, within 1 bf16 ulp). K: [..., n, hd]
+    with any leading dims (e.g. [L, 1, kv, n, hd])."""
+    if delta == 0:
+        return K
+    P = prepared(model)
+    shape = K.shape
+    Kc = K.contiguous().reshape(-1, 1, 1, shape[-2], shape[-1])
+    out = torch.empty_like(Kc)
+    _hip.rope_assemble([(Kc, Kc, 0, delta)], out, torch.empty_like(Kc), P.inv_freq)
+    return out.reshape(shape)
+
+
+def chunk_kv(model, prefix_ids, doc_ids, mode):
+    """tread/blend.py:42-54."""
+    if mode == "shared":
+        K, V = prefill_kv(model, torch.cat([prefix_ids, doc_ids]))
+        P = len(prefix_ids)
+        return [k[:, :, P:] for k in K], [v[:, :, P:] for v in V], P
+    K, V = prefill_kv(model, doc_ids)
+    return K, V, 0
+
+
+def assemble(model, prefix_ids, docs_ids, mode):
+    """tread/blend.py:57-68: exact prefix KV + independently computed doc KV, re-rotated and
+    gathered into one cache by the fused kernel. Returns per-layer K, V lists [1, kv, T, hd]."""
+    P_ = prepared(model)
+    Kp, Vp = prefill_kv(model, prefix_ids)
+    srcs = [(torch.stack(Kp), torch.stack(Vp), 0, 0)]
+    offset = len(prefix_ids)
+    for d in docs_ids:
+        Kd, Vd, base = chunk_kv(model, prefix_ids, d, mode)
+        srcs.append((torch.stack(Kd).contiguous(), torch.stack(Vd).contiguous(), offset, offset - base))
+        offset += len(d)
+    K, V = alloc_cache(P_, offset, prefix_ids.device)
+    _hip.rope_assemble(srcs, K, V, P_.inv_freq)
+    return list(K.unbind(0)), list(V.unbind(0))
+
+
+def _subset_ctx(model, S, T, ref=None):
+    """tread/blend.py:71-79: per-blend constants for positions S: RoPE tables (bf16, rounded as
+    the reference's rotary_emb) and the key ends. No mask tensor: the attention kernel evaluates
+    key <= S[i] itself."""
+    return make_rows(prepared(model), S)
+
+
+def _qkv(layer_idx, model, x, rows, K, V):
+    """tread/blend.py:82-90 fused with the splice of tread/blend.py:106: q/k/v GEMM, RoPE, k/v
+    written into cache rows `rows`. Returns q [n, hq, hd]."""
+    P = prepared(model)
+    lw = P.layers[layer_idx]
+    qkv = F.linear(x, lw.wqkv, lw.bqkv)
+    q = torch.empty(x.shape[0], P.hq, P.hd, dtype=x.dtype, device=x.device)
+    _hip.qkv_rope_splice(qkv, rows.cos, rows.sin, rows.rows, P.hq, P.hkv, P.hd, K, V, q_out=q)
+    return q
+
+
+def _layer_subset(layer_idx, model, h, S, K, V, inplace=False, ctx=None):
+    """tread/blend.py:93-114: recompute decoder layer `layer_idx` for positions S against the full
+    layer cache K, V [1, kv, T, hd]; fresh k/v are spliced at S before attention.
+    h: [1, n, H]. Returns (h, K, V)."""
+    P = prepared(model)
+    R = ctx if ctx is not None else _subset_ctx(model, S, K.shape[2])
+    if not inplace:
+        K, V = K.clone(), V.clone()
+    Kl, Vl = {layer_idx: K}, {layer_idx: V}
+    h2, d = layer_forward(P, layer_idx, h[0].contiguous(), None, R, Kl, Vl)
+    return (h2 + d)[None], K, V
+
+
+def _deviation(P, ctx_ids, Kl, Vl, all_c):
+    """Layer 0 for all candidates (k/v spliced into layer 0 in place), then layer-1 k/v and the
+    fused deviation score. Returns (score bf16 [n], hidden entering layer 1 [n, H], rows)."""
+    R = make_rows(P, all_c)
+    h, d = layer_forward(P, 0, embed(P, ctx_ids[all_c]), None, R, Kl, Vl)
+    lw = P.layers[1]
+    h, x = _hip.add_rmsnorm(h, lw.ln1, P.eps, delta=d)
+    q_rows = P.hq * P.hd
+    kv = F.linear(x, lw.wqkv[q_rows:], None if lw.bqkv is None else lw.bqkv[q_rows:])
+    score = _hip.dev_score(kv, R.cos, R.sin, R.rows, P.hkv, P.hd, Kl[1], Vl[1])
+    return score, h, R
+
+
+def layer1_deviation(model, ctx_ids, K, V, all_c, inplace=False):
+    """tread/blend.py:117-130. Returns (dev [n] bf16, layer-0 hidden [1, n, H], K0, V0)."""
+    P = prepared(model)
+    K, V = list(K), list(V)
+    if not inplace:
+        K[0], V[0] = K[0].clone(), V[0].clone()
+    score, h, _ = _deviation(P, ctx_ids, K, V, all_c)
+    return score, h[None], K[0], V[0]
+
+
+def select(ratio, candidates):
+    """Selection budget of tread/blend.py:144-145 (Python round-half-even)."""
+    n = sum(len(c) for c in candidates)
+    return n, int(round(ratio * n))
+
+
+def blend_cache(model, ctx_ids, K, V, candidates, ratio, policy, gen=None, runner=None, graph=None, T=None,
+                hook=None, trim_last=True):
+    """Selective recompute in place on per-layer cache lists K, V (tread/blend.py:133-179).
+
+    With `graph` (a SubsetRunner bucket whose buffers K, V are) the layer loop is replayed from
+    the captured hipGraph; T is then the context length (rows before the query).
+    `hook(l)`, if given, runs before layer l is first read (lazy assembly of in-flight blocks).
+    With trim_last, the last layer only splices its k/v: its hidden output is discarded by the
+    reference as well, so K/V are unchanged. Returns (S, eff)."""
+    P = prepared(model)
+    dev = K[0].device
+    if not candidates:
+        return torch.empty(0, dtype=torch.long, device=dev), 0.0
+    all_c = torch.cat(candidates)
+    n, budget = select(ratio, candidates)
+    if budget == 0:
+        return all_c[:0], 0.0
+    start = 0
+    if policy == "boundary":
+        rank = torch.cat([torch.arange(len(c), device=c.device) for c in candidates])
+        S = all_c[rank.argsort(stable=True)[:budget]].sort().values
+        h = embed(P, ctx_ids[S])
+    elif policy == "random":
+        S = all_c[torch.randperm(len(all_c), generator=gen, device="cpu").to(dev)[:budget]].sort().values
+        h = embed(P, ctx_ids[S])
+    elif policy == "deviation":
+        if hook is not None:
+            hook(0)
+            hook(1)
+        score, h_all, _ = _deviation(P, ctx_ids, K, V, all_c)
+        sel = _hip.topk_select(score, budget)  # ascending candidate indices => S sorted
+        S = all_c[sel]
+        h = h_all.index_select(0, sel)
+        start = 1
+    else:
+        raise ValueError(policy)
+    if graph is not None:
+        runner.run(graph, h, S, T, hook=hook)
+    else:
+        R = make_rows(P, S)
+        run_layers(P, h, None, R, K, V, range(start, P.L), kv_only_last=trim_last, hook=hook)
+    L = P.L
+    eff = (len(S) * (L - start) + start * n) / (n * L)
+    return S, eff
+
+
+def blend(model, ctx_ids, K, V, candidates, ratio, policy, gen=None, inplace=False, runner=None):
+    """tread/blend.py:133-179 signature: returns (K list, V list, S, eff)."""
+    K, V = list(K), list(V)
+    if not inplace:
+        K, V = [k.clone() for k in K], [v.clone() for v in V]
+    S, eff = blend_cache(model, ctx_ids, K, V, candidates, ratio, policy, gen=gen, runner=None)
+    return K, V, S, eff
+
+
+def to_cache(K, V):
+    """tread/blend.py:182-186: a cache object over per-layer K/V (views, no copy)."""
+    return KVCache.from_layers(K, V)

@@ -1,0 +1,215 @@
+// (a) Fused RoPE re-rotation + gather/append of cached KV blocks into the assembled cache.
+//
+// One streaming pass over HBM: every source row is read once and written once. A work unit is
+// (source, layer, kv head, chunk of ROWS token rows); within a unit the source rows and the
+// destination rows are each one contiguous span, so K and V move as 16-byte vectors with
+// non-temporal loads and stores. K rows of a rotated source are processed as pairs of 16-byte
+// vectors (j, j + hd/2), the two halves that rotate_half mixes. cos/sin are fp32 values of
+// fp32(delta) * inv_freq[j], computed once per work group into LDS while its loads are in flight.
+#include "common.h"
+#include "../../include/tread_hip.h"
+
+namespace tread {
+
+constexpr int ASM_MAX_SRC = 48;
+constexpr int ASM_ROWS = 128;
+constexpr int ASM_THREADS = 256;
+
+struct AsmSrc {
+  const bf16_t* k;
+  const bf16_t* v;
+  int64_t n;
+  int64_t dst_off;
+  int32_t delta;
+  int32_t unit_begin;
+  int32_t chunks;
+  int32_t pad;
+};
+
+struct AsmArgs {
+  AsmSrc src[ASM_MAX_SRC];
+  float inv_freq[64];
+  bf16_t* dk;
+  bf16_t* dv;
+  int64_t t_cap;
+  int32_t n_src;
+  int32_t n_kv;
+  int32_t layer_lo;
+  int32_t n_lr;  // layers in this launch
+  int32_t total_units;
+  int32_t pad;
+};
+
+template <int HD>
+__global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArgs a) {
+  constexpr int HALF = HD / 2;
+  constexpr int KPAIRS = ASM_ROWS * HALF / 8;  // (row, 8-wide column group of the first half)
+  constexpr int KP_PER_T = KPAIRS / ASM_THREADS;
+  constexpr int VCH = ASM_ROWS * HD / 8;  // 16-byte chunks per unit
+  constexpr int V_PER_T = VCH / ASM_THREADS;
+  __shared__ float s_cos[HALF];
+  __shared__ float s_sin[HALF];
+
+  const int u = blockIdx.x;
+  if (u >= a.total_units) return;
+  int s = 0;
+  while (s + 1 < a.n_src && u >= a.src[s + 1].unit_begin) ++s;
+  const AsmSrc& src = a.src[s];
+  const int local = u - src.unit_begin;
+  const int chunk = local % src.chunks;
+  const int lh = local / src.chunks;
+  const int head = lh % a.n_kv;
+  const int layer = a.layer_lo + lh / a.n_kv;
+  const int64_t row0 = (int64_t)chunk * ASM_ROWS;
+  const int rows = (int)min<int64_t>(ASM_ROWS, src.n - row0);
+  const int64_t soff = (((int64_t)layer * a.n_kv + head) * src.n + row0) * HD;
+  const int64_t doff = (((int64_t)layer * a.n_kv + head) * a.t_cap + src.dst_off + row0) * HD;
+  const int tid = threadIdx.x;
+  const int nvec = rows * HD / 8;  // valid 16-byte chunks in this unit
+
+  // V: contiguous span copy.
+  {
+    const u32x4_t* vs = reinterpret_cast<const u32x4_t*>(src.v + soff);
+    u32x4_t* vd = reinterpret_cast<u32x4_t*>(a.dv + doff);
+    u32x4_t buf[V_PER_T];
+#pragma unroll
+    for (int j = 0; j < V_PER_T; ++j) {
+      int c = tid + j * ASM_THREADS;
+      if (c < nvec) buf[j] = ldg_nt(vs + c);
+    }
+    if (src.delta == 0) {
+      // K is a bit copy as well: same span shape as V.
+      const u32x4_t* ks = reinterpret_cast<const u32x4_t*>(src.k + soff);
+      u32x4_t* kd = reinterpret_cast<u32x4_t*>(a.dk + doff);
+      u32x4_t kb[V_PER_T];
+#pragma unroll
+      for (int j = 0; j < V_PER_T; ++j) {
+        int c = tid + j * ASM_THREADS;
+        if (c < nvec) kb[j] = ldg_nt(ks + c);
+      }
+#pragma unroll
+      for (int j = 0; j < V_PER_T; ++j) {
+        int c = tid + j * ASM_THREADS;
+        if (c < nvec) {
+          stg_nt(vd + c, buf[j]);
+          stg_nt(kd + c, kb[j]);
+        }
+      }
+      return;
+    }
+#pragma unroll
+    for (int j = 0; j < V_PER_T; ++j) {
+      int c = tid + j * ASM_THREADS;
+      if (c < nvec) stg_nt(vd + c, buf[j]);
+    }
+  }
+
+  // K with rotation by delta.
+  const bf16_t* ks = src.k + soff;
+  bf16_t* kd = a.dk + doff;
+  u32x4_t x1[KP_PER_T], x2[KP_PER_T];
+#pragma unroll
+  for (int j = 0; j < KP_PER_T; ++j) {
+    int t = tid + j * ASM_THREADS;
+    int r = t / (HALF / 8);
+    int c = (t % (HALF / 8)) * 8;
+    if (r < rows) {
+      x1[j] = ldg_nt(reinterpret_cast<const u32x4_t*>(ks + (int64_t)r * HD + c));
+      x2[j] = ldg_nt(reinterpret_cast<const u32x4_t*>(ks + (int64_t)r * HD + c + HALF));
+    }
+  }
+  if (tid < HALF) {
+    float ang = (float)src.delta * a.inv_freq[tid];
+    float sv, cv;
+    sincosf(ang, &sv, &cv);
+    s_cos[tid] = cv;
+    s_sin[tid] = sv;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < KP_PER_T; ++j) {
+    int t = tid + j * ASM_THREADS;
+    int r = t / (HALF / 8);
+    int c = (t % (HALF / 8)) * 8;
+    if (r < rows) {
+      u32x4_t o1, o2;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        float cl = s_cos[c + 2 * w], ch = s_cos[c + 2 * w + 1];
+        float sl = s_sin[c + 2 * w], sh = s_sin[c + 2 * w + 1];
+        float al = lo_bf(x1[j][w]), ah = hi_bf(x1[j][w]);
+        float bl = lo_bf(x2[j][w]), bh = hi_bf(x2[j][w]);
+        // first half: x1*cos - x2*sin ; second half: x2*cos + x1*sin
+        o1[w] = pack_bf(fmaf(al, cl, -bl * sl), fmaf(ah, ch, -bh * sh));
+        o2[w] = pack_bf(fmaf(bl, cl, al * sl), fmaf(bh, ch, ah * sh));
+      }
+      stg_nt(reinterpret_cast<u32x4_t*>(kd + (int64_t)r * HD + c), o1);
+      stg_nt(reinterpret_cast<u32x4_t*>(kd + (int64_t)r * HD + c + HALF), o2);
+    }
+  }
+}
+
+}  // namespace tread
+
+using namespace tread;
+
+extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void* dst_k, void* dst_v,
+                                        int n_layers, int n_kv, int64_t t_cap, int head_dim,
+                                        const float* inv_freq, int layer_lo, int layer_hi,
+                                        tread_stream_t stream) {
+  if (n_src < 0 || (n_src > 0 && !srcs)) return fail(TREAD_EINVAL, "rope_assemble: bad source list");
+  if (n_src == 0) return 0;
+  if (!dst_k || !dst_v || !inv_freq) return fail(TREAD_EINVAL, "rope_assemble: null pointer");
+  if (head_dim != 64 && head_dim != 128) return fail(TREAD_EINVAL, "rope_assemble: head_dim %d not in {64,128}", head_dim);
+  if (n_kv <= 0 || n_layers <= 0 || t_cap <= 0) return fail(TREAD_EINVAL, "rope_assemble: bad shape");
+  if (layer_lo < 0 || layer_hi > n_layers || layer_lo >= layer_hi)
+    return fail(TREAD_EINVAL, "rope_assemble: layer range [%d,%d) outside [0,%d)", layer_lo, layer_hi, n_layers);
+  for (int i = 0; i < n_src; ++i) {
+    const tread_src_t& s = srcs[i];
+    if (!s.k || !s.v) return fail(TREAD_EINVAL, "rope_assemble: source %d has a null pointer", i);
+    if (s.n_tokens < 0 || s.dst_off < 0 || s.dst_off + s.n_tokens > t_cap)
+      return fail(TREAD_ERANGE, "rope_assemble: source %d rows [%lld,%lld) outside the cache (t_cap %lld)", i,
+                  (long long)s.dst_off, (long long)(s.dst_off + s.n_tokens), (long long)t_cap);
+    if (s.delta > 0x7fffffffLL || s.delta < -0x7fffffffLL)
+      return fail(TREAD_ERANGE, "rope_assemble: source %d delta out of range", i);
+  }
+  const int n_lr = layer_hi - layer_lo;
+  for (int base = 0; base < n_src; base += ASM_MAX_SRC) {
+    AsmArgs a;
+    memset(&a, 0, sizeof(a));
+    int cnt = 0;
+    int64_t units = 0;
+    for (int i = base; i < n_src && cnt < ASM_MAX_SRC; ++i) {
+      const tread_src_t& s = srcs[i];
+      if (s.n_tokens == 0) continue;
+      AsmSrc& d = a.src[cnt++];
+      d.k = (const bf16_t*)s.k;
+      d.v = (const bf16_t*)s.v;
+      d.n = s.n_tokens;
+      d.dst_off = s.dst_off;
+      d.delta = (int32_t)s.delta;
+      d.chunks = (int32_t)((s.n_tokens + ASM_ROWS - 1) / ASM_ROWS);
+      d.unit_begin = (int32_t)units;
+      units += (int64_t)n_lr * n_kv * d.chunks;
+    }
+    if (cnt == 0) continue;
+    if (units > 0x7fffffffLL) return fail(TREAD_ERANGE, "rope_assemble: too many work units");
+    a.n_src = cnt;
+    for (int j = 0; j < head_dim / 2; ++j) a.inv_freq[j] = inv_freq[j];
+    a.dk = (bf16_t*)dst_k;
+    a.dv = (bf16_t*)dst_v;
+    a.t_cap = t_cap;
+    a.n_kv = n_kv;
+    a.layer_lo = layer_lo;
+    a.n_lr = n_lr;
+    a.total_units = (int32_t)units;
+    dim3 grid((unsigned)units), block(ASM_THREADS);
+    if (head_dim == 128)
+      hipLaunchKernelGGL(rope_assemble_kernel<128>, grid, block, 0, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL(rope_assemble_kernel<64>, grid, block, 0, (hipStream_t)stream, a);
+    int rc = check_launch("rope_assemble");
+    if (rc) return rc;
+  }
+  return 0;
+}

@@ -1,0 +1,240 @@
+"""Reuse engine: build a request's KV cache from content-addressed blocks (tread/engine.py).
+
+Request = [prefix][doc_1]...[doc_N][query] as separate segments (tread/engine.py:1-7). The prefix
+is an exact-prefix block; every doc block is computed once on top of the prefix at base position
+P, cached under a key chained on the prefix key, and re-rotated to wherever it lands later.
+
+Same API, keys, hit/miss accounting and stage timings as the reference; what runs underneath:
+  - assembly: ONE fused HIP launch rotates every doc block by (offset - base) and gathers it,
+    with the prefix block, into a preallocated [L, 1, kv, T + Nq, hd] cache (kernel (a)).
+    Blocks still arriving from the host tier are assembled per layer, right before the layer is
+    first read, after waiting that layer's copy event (overlap of DMA and compute);
+  - blend: deviation pass + top-k (kernel (b)) and the recompute loop with the MFMA attention
+    (kernel (c)), eager or replayed from a hipGraph whose static buffer is the cache itself;
+  - query: the query rows are appended in place at rows T.. of the same cache (no cat/copy).
+  - cold path: all missed docs in one packed forward whose attention is block-diagonal in-kernel
+    (each doc sees the prefix and itself), no [n, P + n] mask tensor.
+Stage boundaries synchronise the current stream only, so copies on the store's copy stream keep
+overlapping compute across them.
+"""
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from tread_amd import _hip
+from tread_amd.blend import blend_cache, forward_into, prepared, select
+from tread_amd.cache import KVCache
+from tread_amd.forward import alloc_cache, embed, final_logits, make_rows, run_layers
+from tread_amd.graphs import SubsetRunner
+from tread_amd.model import rope_theta_of
+from tread_amd.store import BlockStore, block_key
+
+
+@dataclass
+class RequestStats:
+    """tread/engine.py:19-26."""
+    hits: int = 0
+    misses: int = 0
+    tokens_reused: int = 0
+    tokens_prefilled: int = 0
+    recompute_eff: float = 0.0
+    t: dict = field(default_factory=dict)  # stage -> seconds
+
+
+class _Tmp:
+    """tread/engine.py:169-173: an uncached block (store budget too small): Block's fields."""
+
+    def __init__(self, K, V, base):
+        self.K, self.V, self.base, self.n_tokens = K, V, base, K.shape[-2]
+        self.ready = None
+
+    def wait(self, layers=None, stream=None):
+        pass
+
+
+def model_sig(model):
+    """tread/engine.py:36-38: (name_or_path, str(dtype), rope_theta, rope_scaling). The theta is
+    read from rope_parameters when the config keeps it there, so keys match a config that carries
+    it as rope_theta; default RoPE counts as no scaling."""
+    cfg = model.config
+    scaling = getattr(cfg, "rope_scaling", None)
+    if isinstance(scaling, dict) and scaling.get("rope_type", scaling.get("type")) == "default":
+        scaling = None
+    return (getattr(cfg, "_name_or_path", ""), str(model.dtype), rope_theta_of(cfg), scaling)
+
+
+class _Assembly:
+    """Rotate+gather of the request's blocks into the cache; per-layer for in-flight blocks."""
+
+    def __init__(self, P, K, V, sources):
+        self.P, self.K, self.V = P, K, V
+        ready = [(b.K, b.V, off, delta) for b, off, delta in sources if getattr(b, "ready", None) is None]
+        self.pending = [(b, off, delta) for b, off, delta in sources if getattr(b, "ready", None) is not None]
+        self.done = [False] * P.L
+        if ready:
+            _hip.rope_assemble(ready, K, V, P.inv_freq)
+        if not self.pending:
+            self.done = [True] * P.L
+
+    def ensure(self, l):
+        if self.done[l]:
+            return
+        for b, _, _ in self.pending:
+            b.wait([l])
+        _hip.rope_assemble([(b.K, b.V, off, delta) for b, off, delta in self.pending], self.K, self.V,
+                           self.P.inv_freq, layer_lo=l, layer_hi=l + 1)
+        self.done[l] = True
+
+    def finish(self):
+        for l in range(self.P.L):
+            self.ensure(l)
+
+
+class Engine:
+    def __init__(self, model, store: BlockStore, graphs=False):
+        self.model = model
+        self.store = store
+        self.P = prepared(model)
+        # hipGraph replay of the recompute loop (tread/graphs.py); off by default as in the
+        # reference, since each new size bucket pays a one-off capture.
+        self.runner = SubsetRunner(model) if graphs else None
+        self.sig = model_sig(model)
+        self.last_selected = None  # positions recomputed by the last prefill (diagnostics)
+
+    def _sync(self):
+        torch.cuda.current_stream().synchronize()
+
+    @torch.inference_mode()
+    def prefix_block(self, prefix_ids, st, namespace=""):
+        """tread/engine.py:44-57."""
+        key = block_key(*self.sig, namespace, "prefix", prefix_ids)
+        b = self.store.get(key)
+        if b is None:
+            st.misses += 1
+            st.tokens_prefilled += len(prefix_ids)
+            K, V = alloc_cache(self.P, len(prefix_ids), prefix_ids.device)
+            forward_into(self.model, prefix_ids, K, V, want_logits=False)
+            b = self.store.put(key, K, V, 0) or _Tmp(K, V, 0)
+        else:
+            st.hits += 1
+            st.tokens_reused += len(prefix_ids)
+        return key, b
+
+    @torch.inference_mode()
+    def doc_blocks(self, prefix_key, pb, docs, st):
+        """tread/engine.py:59-96: look up every doc; prefill all misses in one packed forward.
+
+        The packed sequence sits on top of the prefix rows of a temporary cache; token j of doc i
+        has RoPE position P + j, writes cache row P + off_i + j, and sees rows [0, P) plus
+        [P + off_i, P + off_i + j]: the reference's block-diagonal mask, evaluated in-kernel."""
+        keys = [block_key(*self.sig, prefix_key, d) for d in docs]
+        blocks = [self.store.get(k) for k in keys]
+        miss = [i for i, b in enumerate(blocks) if b is None]
+        st.hits += len(docs) - len(miss)
+        st.tokens_reused += sum(len(d) for d, b in zip(docs, blocks) if b is not None)
+        if not miss:
+            return blocks
+        st.misses += len(miss)
+        P = pb.n_tokens
+        ids = torch.cat([docs[i] for i in miss])
+        n, dev = len(ids), ids.device
+        st.tokens_prefilled += n
+        lens = [len(docs[i]) for i in miss]
+        offs = [0]
+        for Ld in lens[:-1]:
+            offs.append(offs[-1] + Ld)
+        local = torch.cat([torch.arange(Ld, device=dev) for Ld in lens])
+        seg0 = torch.cat([torch.full((Ld,), P + o, device=dev, dtype=torch.int64) for Ld, o in zip(lens, offs)])
+        K, V = alloc_cache(self.P, P + n, dev)
+        pb.wait()
+        _hip.rope_assemble([(pb.K, pb.V, 0, 0)], K, V, self.P.inv_freq)
+        forward_into(self.model, ids, K, V, start_row=P, pos=P + local, kseg=seg0, n_shared=P, want_logits=False)
+        for i, o, Ld in zip(miss, offs, lens):
+            Kd = K[..., P + o:P + o + Ld, :].contiguous()
+            Vd = V[..., P + o:P + o + Ld, :].contiguous()
+            blocks[i] = self.store.put(keys[i], Kd, Vd, P) or _Tmp(Kd, Vd, P)
+        return blocks
+
+    @torch.inference_mode()
+    def prefill(self, prefix_ids, docs, query_ids, ratio=0.0, policy="deviation", namespace="", gen=None):
+        """tread/engine.py:98-136. Returns (logits [vocab], KVCache, RequestStats)."""
+        st = RequestStats()
+        self._sync()
+        t0 = time.perf_counter()
+
+        pkey, pb = self.prefix_block(prefix_ids, st, namespace)
+        blocks = self.doc_blocks(pkey, pb, docs, st)
+        Pn = pb.n_tokens
+        T = Pn + sum(len(d) for d in docs)
+        Nq = len(query_ids)
+        dev = prefix_ids.device
+        graph = None
+        if ratio > 0 and self.runner is not None and docs and self.runner.worth_it(T):
+            n, budget = select(ratio, docs)
+            if budget > 0:
+                start = 1 if policy == "deviation" else 0
+                graph = self.runner.cache_for(start, budget, T, Nq, dev)
+        if graph is not None:
+            K, V = graph.K, graph.V
+        else:
+            K, V = alloc_cache(self.P, T + Nq, dev)
+        sources = [(pb, 0, 0)]
+        cands = []
+        offset = Pn
+        for d, b in zip(docs, blocks):
+            sources.append((b, offset, offset - b.base))
+            cands.append(torch.arange(offset, offset + len(d), device=d.device))
+            offset += len(d)
+        asm = _Assembly(self.P, K, V, sources)
+        Kl, Vl = K.unbind(0), V.unbind(0)
+        self._sync()
+        t1 = time.perf_counter()
+
+        self.last_selected = None
+        if ratio > 0:
+            ctx = torch.cat([prefix_ids] + list(docs))
+            self.last_selected, st.recompute_eff = blend_cache(self.model, ctx, Kl, Vl, cands, ratio, policy, gen=gen,
+                                              runner=self.runner, graph=graph, T=T, hook=asm.ensure)
+        self._sync()
+        t2 = time.perf_counter()
+
+        R = make_rows(self.P, torch.arange(T, T + Nq, device=dev))
+        h, d = run_layers(self.P, embed(self.P, query_ids), None, R, Kl, Vl, range(self.P.L), hook=asm.ensure)
+        logits = final_logits(self.P, h, d)
+        self._sync()
+        t3 = time.perf_counter()
+        st.t = dict(assemble=t1 - t0, blend=t2 - t1, query=t3 - t2, ttft=t3 - t0)
+        return logits, KVCache(K, V, T + Nq), st
+
+    @torch.inference_mode()
+    def prefill_prefix_only(self, prefix_ids, docs, query_ids):
+        """tread/engine.py:138-152: exact-prefix caching only; every doc is prefilled again."""
+        st = RequestStats()
+        self._sync()
+        t0 = time.perf_counter()
+        _, pb = self.prefix_block(prefix_ids, st)
+        rest = torch.cat(list(docs) + [query_ids])
+        st.tokens_prefilled += len(rest) - len(query_ids)
+        Pn = pb.n_tokens
+        K, V = alloc_cache(self.P, Pn + len(rest), prefix_ids.device)
+        pb.wait()
+        _hip.rope_assemble([(pb.K, pb.V, 0, 0)], K, V, self.P.inv_freq)
+        logits = forward_into(self.model, rest, K, V, start_row=Pn)
+        self._sync()
+        st.t = dict(ttft=time.perf_counter() - t0)
+        return logits, KVCache(K, V, Pn + len(rest)), st
+
+
+@torch.inference_mode()
+def prefill_full(model, prefix_ids, docs, query_ids):
+    """tread/engine.py:155-166: no caching at all (the TTFT denominator)."""
+    torch.cuda.current_stream().synchronize()
+    t0 = time.perf_counter()
+    ids = torch.cat([prefix_ids] + list(docs) + [query_ids])
+    P = prepared(model)
+    K, V = alloc_cache(P, len(ids), ids.device)
+    logits = forward_into(model, ids, K, V)
+    torch.cuda.current_stream().synchronize()
+    st = RequestStats(tokens_prefilled=len(ids) - len(query_ids), t=dict(ttft=time.perf_counter() - t0))
+    return logits, KVCache(K, V, len(ids)), st

@@ -1,0 +1,93 @@
+"""Decoder forward over an arbitrary set of token rows against a preallocated KV cache.
+
+Every forward on the path is the same computation with different row sets:
+  - recompute of positions S (tread/blend.py:93-114): rows = positions = S, keys <= S[i];
+  - the deviation pass over all candidates (tread/blend.py:117-130);
+  - the query forward over the assembled cache (tread/engine.py:256-257): rows T..T+Nq-1;
+  - prefix / full prefill (tread/blend.py:12-19; tread/engine.py:155-166): rows 0..N-1;
+  - the packed cold prefill of missed docs (tread/engine.py:200-213): rows after the prefix,
+    RoPE positions restarting at P per doc, keys = prefix + own doc (block-diagonal).
+A layer is: fused residual-add + RMSNorm (HIP) -> one q|k|v GEMM (hipBLASLt via torch) ->
+RoPE + splice of k/v into the cache (HIP) -> MFMA attention (HIP) -> o_proj GEMM -> fused add +
+RMSNorm (HIP) -> gate|up GEMM -> SiLU-mul (HIP) -> down GEMM. The MLP output is carried as a
+pending residual `delta` that the next layer's norm kernel adds.
+"""
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from tread_amd import _hip
+
+
+@dataclass
+class Rows:
+    rows: torch.Tensor            # int64 [n]: cache row receiving token i's k/v
+    kend: torch.Tensor            # int64 [n]: last cache row token i may attend to
+    cos: torch.Tensor             # bf16 [n, hd/2]: RoPE of token i's position
+    sin: torch.Tensor
+    kseg: Optional[torch.Tensor] = None  # int64 [n]: first row of token i's own segment
+    n_shared: int = 0             # rows [0, n_shared) are visible to every token (with kseg)
+
+    def __len__(self):
+        return self.rows.numel()
+
+
+def make_rows(P, rows, pos=None, kseg=None, n_shared=0):
+    """RoPE tables for `pos` (default: rows) and causal key ends = rows."""
+    rows = rows.to(torch.int64).contiguous()
+    pos = rows if pos is None else pos.to(torch.int64).contiguous()
+    cos, sin = _hip.rope_table(pos, P.inv_freq, P.hd)
+    return Rows(rows=rows, kend=rows, cos=cos, sin=sin, kseg=kseg, n_shared=n_shared)
+
+
+def layer_forward(P, l, h, delta, R: Rows, K, V, kv_only=False):
+    """One decoder layer for rows R. h, delta: [n, H] (delta may be None). K, V: per-layer
+    sequences of [1, hkv, t_cap, hd] cache tensors; layer l receives the rows' k/v.
+    Returns (h, delta) entering layer l+1, or (h, None) when kv_only (k/v spliced, nothing else)."""
+    lw = P.layers[l]
+    hq, hkv, hd = P.hq, P.hkv, P.hd
+    h, x = _hip.add_rmsnorm(h, lw.ln1, P.eps, delta=delta)
+    n = h.shape[0]
+    if kv_only:
+        q_rows = hq * hd
+        kv = F.linear(x, lw.wqkv[q_rows:], None if lw.bqkv is None else lw.bqkv[q_rows:])
+        _hip.qkv_rope_splice(kv, R.cos, R.sin, R.rows, hq, hkv, hd, K[l], V[l], q_out=None, k_col=0)
+        return h, None
+    qkv = F.linear(x, lw.wqkv, lw.bqkv)
+    q = torch.empty(n, hq, hd, dtype=h.dtype, device=h.device)
+    _hip.qkv_rope_splice(qkv, R.cos, R.sin, R.rows, hq, hkv, hd, K[l], V[l], q_out=q)
+    o = _hip.subset_attn(q, K[l], V[l], R.kend, hq, hkv, hd, P.scale, kseg=R.kseg, n_shared=R.n_shared)
+    a = F.linear(o, lw.wo)
+    h, x = _hip.add_rmsnorm(h, lw.ln2, P.eps, delta=a)
+    m = _hip.silu_mul(F.linear(x, lw.wgu))
+    return h, F.linear(m, lw.wd)
+
+
+def run_layers(P, h, delta, R, K, V, layers, kv_only_last=False, hook=None):
+    """Run `layers` (an ordered range) for rows R; `hook(l)` runs before layer l (lazy assembly).
+    With kv_only_last, the last layer only splices its k/v (its hidden output is never used)."""
+    layers = list(layers)
+    for j, l in enumerate(layers):
+        if hook is not None:
+            hook(l)
+        h, delta = layer_forward(P, l, h, delta, R, K, V, kv_only=kv_only_last and j == len(layers) - 1)
+    return h, delta
+
+
+def final_logits(P, h, delta):
+    """Final RMSNorm + lm_head on the last row only (num_logits_to_keep=1). Returns [vocab]."""
+    _, x = _hip.add_rmsnorm(h[-1:].contiguous(), P.norm, P.eps,
+                            delta=None if delta is None else delta[-1:].contiguous())
+    return F.linear(x, P.lm_head)[0]
+
+
+def embed(P, ids):
+    return F.embedding(ids, P.embed)
+
+
+def alloc_cache(P, t_cap, device):
+    shape = (P.L, 1, P.hkv, t_cap, P.hd)
+    return (torch.empty(shape, dtype=P.embed.dtype, device=device),
+            torch.empty(shape, dtype=P.embed.dtype, device=device))

@@ -1,0 +1,114 @@
+"""hipGraph replay of the selective-recompute layer loop (tread/graphs.py, redesigned).
+
+The reference captures layers start..L-1 per padded size bucket, but copies the whole cache into
+the graph's static buffers before each replay and back out after, which made graphs lose above
+2k tokens (tread/graphs.py:64-67,92-99). Here the static buffer of a bucket IS the assembled
+cache: the engine asks the runner for it before assembly (`cache_for`), the fused assemble kernel
+writes the request's blocks straight into it, and a replay only needs the selected positions S
+and their hidden rows copied in (a few MB). Padding follows the reference: padded query slots
+sit at positions T, T+1, ... inside the bucket's spare rows, which no real query can see.
+
+Each bucket holds one [L, 1, kv, t_cap, hd] K/V pair; the cache returned by the engine aliases
+it and stays valid until the next request replays the same bucket.
+"""
+from collections import OrderedDict
+
+import torch
+
+from tread_amd.forward import alloc_cache, make_rows, run_layers
+
+
+def _bucket(n, T, n_min=64, n_step=256, t_step=1024):
+    """tread/graphs.py:22-27: rows padded to a power of two >= n_min up to n_step, then to a
+    multiple of n_step; cache length padded so the padded slots fit, to a multiple of t_step."""
+    if n <= n_step:
+        nb = max(n_min, 1 << (n - 1).bit_length())
+    else:
+        nb = -(-n // n_step) * n_step
+    Tb = -(-(T + nb - n) // t_step) * t_step
+    return nb, Tb
+
+
+def _q_room(n_query):
+    return 256 * max(1, -(-n_query // 256))
+
+
+class _Graph:
+    def __init__(self, P, start, nb, Tb, t_cap, device, trim_last):
+        self.K, self.V = alloc_cache(P, t_cap, device)
+        self.K.zero_()
+        self.V.zero_()
+        self.Kl, self.Vl = self.K.unbind(0), self.V.unbind(0)
+        self.h = torch.zeros(nb, P.H, dtype=P.embed.dtype, device=device)
+        self.S = torch.arange(nb, dtype=torch.int64, device=device)
+        self.nb, self.Tb, self.start = nb, Tb, start
+
+        def body():
+            R = make_rows(P, self.S)
+            return run_layers(P, self.h, None, R, self.Kl, self.Vl, range(start, P.L), kv_only_last=trim_last)
+
+        s = torch.cuda.Stream(device=device)  # default priority
+        s.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                body()
+        torch.cuda.current_stream(device).wait_stream(s)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = body()
+
+
+class SubsetRunner:
+    """One captured graph per (start layer, rows bucket, cache bucket, query room); LRU of
+    `max_graphs`. `max_ctx`: contexts above it run eagerly (None: always graph)."""
+
+    def __init__(self, model, max_graphs=4, max_ctx=None, trim_last=True):
+        from tread_amd.blend import prepared
+        self.model = model
+        self.P = prepared(model)
+        self.max_graphs = max_graphs
+        self.max_ctx = max_ctx
+        self.trim_last = trim_last
+        self.graphs: "OrderedDict[tuple, _Graph]" = OrderedDict()
+        self.captures = 0
+
+    def worth_it(self, T):
+        return self.max_ctx is None or T <= self.max_ctx
+
+    def _graph(self, start, n, T, n_query, device):
+        nb, Tb = _bucket(n, T)
+        key = (start, nb, Tb, _q_room(n_query))
+        g = self.graphs.get(key)
+        if g is None:
+            while len(self.graphs) >= self.max_graphs:
+                self.graphs.popitem(last=False)
+            g = _Graph(self.P, start, nb, Tb, Tb + key[3], device, self.trim_last)
+            self.graphs[key] = g
+            self.captures += 1
+        self.graphs.move_to_end(key)
+        return g
+
+    @torch.inference_mode()
+    def cache_for(self, start, n, T, n_query, device):
+        """The bucket graph serving a request that recomputes n rows from layer `start` over a
+        T-row context followed by n_query query rows; its .K/.V are the cache to assemble into."""
+        return self._graph(start, n, T, n_query, device)
+
+    @torch.inference_mode()
+    def run(self, g, h, S, T, hook=None):
+        """Replay layers start..L-1 of bucket graph `g` for sorted positions S (len n <= g.nb) with
+        hidden rows h [n, H] over a T-row context. `hook(l)` runs for every layer first (lazy
+        assembly must complete before the replay reads the cache)."""
+        n = len(S)
+        if n > g.nb or T + g.nb - n > g.Tb:
+            raise ValueError(f"request (n={n}, T={T}) does not fit bucket (nb={g.nb}, Tb={g.Tb})")
+        if hook is not None:
+            for l in range(g.start, self.P.L):
+                hook(l)
+        g.S[:n].copy_(S)
+        g.h[:n].copy_(h)
+        if n < g.nb:
+            g.S[n:].copy_(torch.arange(T, T + g.nb - n, device=S.device))
+            g.h[n:].zero_()
+        g.graph.replay()
+        return g.out
