@@ -32,9 +32,11 @@ int tread_abi_version(void);
  * tread/engine.py:233-245 (torch.cat of the prefix and rotated doc blocks along T, then unbind).
  * Source i holds K and V as [n_layers, n_kv, n_tokens, head_dim]; its rows land at destination
  * rows [dst_off, dst_off + n_tokens) of dst [n_layers, n_kv, t_cap, head_dim]. K is rotated by
- * `delta` positions with fp32 cos/sin of fp32(delta) * inv_freq[j] and one RNE rounding to bf16;
- * delta == 0 and V are bit copies. Only layers [layer_lo, layer_hi) are written.
- * inv_freq: HOST array of head_dim/2 fp32 values (passed by value to the kernel).
+ * `delta` positions: with c, s = cos_sin[i][j] (device fp32 [n_src][head_dim/2][2], the cos and sin
+ * of fp32(delta_i) * inv_freq[j] as the reference's rotary embedding computes them), row element j
+ * becomes fl(fl(x_j*c) + fl(-x_{j+hd/2}*s)) and element j+hd/2 fl(fl(x_{j+hd/2}*c) + fl(x_j*s)),
+ * rounded once to bf16 (the fp32 reference rotation, op for op). delta == 0 and V are bit copies.
+ * Only layers [layer_lo, layer_hi) are written.
  * srcs: HOST array (copied into the kernel arguments; at most 48 sources per internal launch).
  */
 typedef struct tread_src {
@@ -46,7 +48,7 @@ typedef struct tread_src {
 } tread_src_t;
 
 int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void* dst_k, void* dst_v, int n_layers,
-                             int n_kv, int64_t t_cap, int head_dim, const float* inv_freq, int layer_lo,
+                             int n_kv, int64_t t_cap, int head_dim, const float* cos_sin, int layer_lo,
                              int layer_hi, tread_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------

@@ -95,9 +95,19 @@ def _freq(inv_freq):
 
 # ------------------------------------------------------------------------------------------- (a)
 
-def rope_assemble(sources, dst_k, dst_v, inv_freq, layer_lo=0, layer_hi=None):
+def delta_table(inv_freq, deltas, device):
+    """fp32 [n, hd/2, 2] (cos, sin) of fp32(delta) * inv_freq, computed with the same torch ops as
+    the reference's rotary embedding (fp32 outer product, then cos / sin), moved to `device`."""
+    pos = torch.tensor([int(d) for d in deltas], dtype=torch.int64)
+    freqs = (inv_freq.detach().to("cpu", torch.float32)[:, None] @ pos[None, :].float()).transpose(0, 1)
+    tab = torch.stack([freqs.cos(), freqs.sin()], dim=-1).contiguous()
+    return tab.pin_memory().to(device, non_blocking=True)
+
+
+def rope_assemble(sources, dst_k, dst_v, inv_freq, layer_lo=0, layer_hi=None, table=None):
     """sources: list of (K, V, dst_off, delta) with K, V [L, 1, kv, n, hd] bf16 on the GPU.
-    dst_k, dst_v: [L, 1, kv, t_cap, hd]. Rotates K by delta (fp32 cos/sin), copies V."""
+    dst_k, dst_v: [L, 1, kv, t_cap, hd]. Rotates K by delta (fp32 cos/sin table), copies V.
+    `table` (from delta_table over the sources' deltas) may be passed to reuse it across calls."""
     _need(dst_k, "dst_k")
     _need(dst_v, "dst_v")
     L, one, kv, t_cap, hd = dst_k.shape
@@ -111,9 +121,14 @@ def rope_assemble(sources, dst_k, dst_v, inv_freq, layer_lo=0, layer_hi=None):
         if K.shape[:3] != (L, 1, kv) or K.shape[-1] != hd or V.shape != K.shape:
             raise ValueError(f"source {i}: shape {tuple(K.shape)} does not match cache {tuple(dst_k.shape)}")
         arr[i] = Src(K.data_ptr(), V.data_ptr(), K.shape[-2], int(off), int(delta))
-    f, fp = _freq(inv_freq)
+    if table is None:
+        table = delta_table(inv_freq, [s[3] for s in sources], dst_k.device)
+    if table.shape != (len(sources), hd // 2, 2) or table.dtype != torch.float32 or not table.is_cuda:
+        raise ValueError("rope_assemble: table must be fp32 [n_src, hd/2, 2] on the GPU")
     _check("tread_rope_assemble_bf16", lib().tread_rope_assemble_bf16(
-        arr, len(sources), _ptr(dst_k), _ptr(dst_v), L, kv, t_cap, hd, fp, layer_lo, layer_hi, _stream()))
+        arr, len(sources), _ptr(dst_k), _ptr(dst_v), L, kv, t_cap, hd,
+        ctypes.cast(table.data_ptr(), P_F32), layer_lo, layer_hi, _stream()))
+    return table
 
 
 # ------------------------------------------------------------------------------------ RoPE / glue

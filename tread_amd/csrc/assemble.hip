@@ -4,8 +4,10 @@
 // (source, layer, kv head, chunk of ROWS token rows); within a unit the source rows and the
 // destination rows are each one contiguous span, so K and V move as 16-byte vectors with
 // non-temporal loads and stores. K rows of a rotated source are processed as pairs of 16-byte
-// vectors (j, j + hd/2), the two halves that rotate_half mixes. cos/sin are fp32 values of
-// fp32(delta) * inv_freq[j], computed once per work group into LDS while its loads are in flight.
+// vectors (j, j + hd/2), the two halves that rotate_half mixes. cos/sin come from a per-source fp32
+// table (the caller builds it exactly as the reference's rotary embedding does) and are staged in LDS
+// while the work group's loads are in flight. The rotation keeps the reference's fp32 op order with
+// no contraction, fl(fl(x1*c) + fl(-x2*s)) and fl(fl(x2*c) + fl(x1*s)), then one RNE to bf16.
 #include "common.h"
 #include "../../include/tread_hip.h"
 
@@ -28,7 +30,7 @@ struct AsmSrc {
 
 struct AsmArgs {
   AsmSrc src[ASM_MAX_SRC];
-  float inv_freq[64];
+  const float* cos_sin;  // [n_src][HD/2][2]: cos, sin of this launch's sources
   bf16_t* dk;
   bf16_t* dv;
   int64_t t_cap;
@@ -119,11 +121,9 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArg
     }
   }
   if (tid < HALF) {
-    float ang = (float)src.delta * a.inv_freq[tid];
-    float sv, cv;
-    sincosf(ang, &sv, &cv);
-    s_cos[tid] = cv;
-    s_sin[tid] = sv;
+    const float* cs = a.cos_sin + ((int64_t)s * HALF + tid) * 2;
+    s_cos[tid] = cs[0];
+    s_sin[tid] = cs[1];
   }
   __syncthreads();
 #pragma unroll
@@ -139,9 +139,13 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArg
         float sl = s_sin[c + 2 * w], sh = s_sin[c + 2 * w + 1];
         float al = lo_bf(x1[j][w]), ah = hi_bf(x1[j][w]);
         float bl = lo_bf(x2[j][w]), bh = hi_bf(x2[j][w]);
-        // first half: x1*cos - x2*sin ; second half: x2*cos + x1*sin
-        o1[w] = pack_bf(fmaf(al, cl, -bl * sl), fmaf(ah, ch, -bh * sh));
-        o2[w] = pack_bf(fmaf(bl, cl, al * sl), fmaf(bh, ch, ah * sh));
+        // first half: x1*cos + (-x2)*sin ; second half: x2*cos + x1*sin; each product and sum
+        // rounded to fp32 on its own, as the reference's separate torch ops do
+        {
+#pragma clang fp contract(off)
+          o1[w] = pack_bf(al * cl + (-bl) * sl, ah * ch + (-bh) * sh);
+          o2[w] = pack_bf(bl * cl + al * sl, bh * ch + ah * sh);
+        }
       }
       stg_nt(reinterpret_cast<u32x4_t*>(kd + (int64_t)r * HD + c), o1);
       stg_nt(reinterpret_cast<u32x4_t*>(kd + (int64_t)r * HD + c + HALF), o2);
@@ -155,11 +159,11 @@ using namespace tread;
 
 extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void* dst_k, void* dst_v,
                                         int n_layers, int n_kv, int64_t t_cap, int head_dim,
-                                        const float* inv_freq, int layer_lo, int layer_hi,
+                                        const float* cos_sin, int layer_lo, int layer_hi,
                                         tread_stream_t stream) {
   if (n_src < 0 || (n_src > 0 && !srcs)) return fail(TREAD_EINVAL, "rope_assemble: bad source list");
   if (n_src == 0) return 0;
-  if (!dst_k || !dst_v || !inv_freq) return fail(TREAD_EINVAL, "rope_assemble: null pointer");
+  if (!dst_k || !dst_v || !cos_sin) return fail(TREAD_EINVAL, "rope_assemble: null pointer");
   if (head_dim != 64 && head_dim != 128) return fail(TREAD_EINVAL, "rope_assemble: head_dim %d not in {64,128}", head_dim);
   if (n_kv <= 0 || n_layers <= 0 || t_cap <= 0) return fail(TREAD_EINVAL, "rope_assemble: bad shape");
   if (layer_lo < 0 || layer_hi > n_layers || layer_lo >= layer_hi)
@@ -179,9 +183,9 @@ extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void
     memset(&a, 0, sizeof(a));
     int cnt = 0;
     int64_t units = 0;
-    for (int i = base; i < n_src && cnt < ASM_MAX_SRC; ++i) {
+    const int end = n_src < base + ASM_MAX_SRC ? n_src : base + ASM_MAX_SRC;
+    for (int i = base; i < end; ++i) {  // empty sources keep their slot: table row == source index
       const tread_src_t& s = srcs[i];
-      if (s.n_tokens == 0) continue;
       AsmSrc& d = a.src[cnt++];
       d.k = (const bf16_t*)s.k;
       d.v = (const bf16_t*)s.v;
@@ -192,10 +196,10 @@ extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void
       d.unit_begin = (int32_t)units;
       units += (int64_t)n_lr * n_kv * d.chunks;
     }
-    if (cnt == 0) continue;
+    if (units == 0) continue;
     if (units > 0x7fffffffLL) return fail(TREAD_ERANGE, "rope_assemble: too many work units");
     a.n_src = cnt;
-    for (int j = 0; j < head_dim / 2; ++j) a.inv_freq[j] = inv_freq[j];
+    a.cos_sin = cos_sin + (int64_t)base * (head_dim / 2) * 2;
     a.dk = (bf16_t*)dst_k;
     a.dv = (bf16_t*)dst_v;
     a.t_cap = t_cap;

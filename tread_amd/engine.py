@@ -72,6 +72,7 @@ class _Assembly:
         ready = [(b.K, b.V, off, delta) for b, off, delta in sources if getattr(b, "ready", None) is None]
         self.pending = [(b, off, delta) for b, off, delta in sources if getattr(b, "ready", None) is not None]
         self.done = [False] * P.L
+        self.table = None
         if ready:
             _hip.rope_assemble(ready, K, V, P.inv_freq)
         if not self.pending:
@@ -82,8 +83,8 @@ class _Assembly:
             return
         for b, _, _ in self.pending:
             b.wait([l])
-        _hip.rope_assemble([(b.K, b.V, off, delta) for b, off, delta in self.pending], self.K, self.V,
-                           self.P.inv_freq, layer_lo=l, layer_hi=l + 1)
+        self.table = _hip.rope_assemble([(b.K, b.V, off, delta) for b, off, delta in self.pending], self.K, self.V,
+                                        self.P.inv_freq, layer_lo=l, layer_hi=l + 1, table=self.table)
         self.done[l] = True
 
     def finish(self):
