@@ -102,10 +102,14 @@ int tread_topk_select_bf16(const void* score, int64_t n, int64_t k, int64_t* sel
  * (tread/engine.py:206-213,257). Row i of q [n, hq, head_dim] sees cache key j of its KV head
  * iff j <= kend[i] and (j < n_shared or j >= kseg[i]); kseg may be NULL (then keys [0, kend[i]]).
  * out: [n, hq * head_dim]. scale: softmax scale (head_dim^-0.5). head_dim: 64 or 128.
+ * Few rows over a long cache (the query forward) split the key axis across work groups; that needs
+ * ws of tread_subset_attn_workspace_bytes(...) bytes (device). With ws NULL or too small the call
+ * still succeeds, unsplit.
  */
+size_t tread_subset_attn_workspace_bytes(int64_t n, int hq, int hkv, int head_dim, int64_t t_cap);
 int tread_subset_attn_bf16(const void* q, const void* k_cache, const void* v_cache, const int64_t* kend,
                            const int64_t* kseg, int64_t n_shared, int64_t n, int hq, int hkv, int head_dim,
-                           int64_t t_cap, float scale, void* out, tread_stream_t stream);
+                           int64_t t_cap, float scale, void* out, void* ws, size_t ws_bytes, tread_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Decoder-layer glue for the recompute rows (transformers Qwen2RMSNorm / Qwen2MLP as called at

@@ -255,6 +255,11 @@ CASES = [
     (64, 8, 128, 1500, 90, "subset"),
     (8, 2, 128, 700, 337, "segments"),
     (14, 2, 64, 500, 230, "segments"),
+    # few rows over a long cache: split-K + combine
+    (28, 4, 128, 20000, 32, "query"),
+    (14, 2, 64, 9000, 5, "query"),
+    (28, 4, 128, 6000, 40, "subset"),
+    (64, 8, 128, 33000, 17, "query"),
 ]
 
 
@@ -269,6 +274,8 @@ def test_subset_attention_vs_textbook(hq, hkv, hd, t_cap, n, kind):
         kend = torch.sort(torch.randperm(t_cap, generator=g)[:n]).values
     elif kind == "prefill":
         kend = torch.arange(n)
+    elif kind == "query":  # the query rows at the end of the cache
+        kend = torch.arange(t_cap - n, t_cap)
     else:  # packed docs on a shared prefix: block-diagonal visibility
         n_shared = 40
         lens = [100, 37, n - 137]

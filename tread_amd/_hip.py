@@ -10,7 +10,7 @@ from pathlib import Path
 import torch  # loads torch's HIP runtime first, so the library below binds to the same one
 
 LIB_PATH = Path(__file__).resolve().with_name("libtread_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 c_i64, c_int, c_void, c_float, c_size = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
 P_I64 = ctypes.POINTER(ctypes.c_int64)
@@ -34,8 +34,9 @@ _SIGS = {
                                      c_void, c_i64, c_void, c_void]),
     "tread_topk_workspace_bytes": (c_size, [c_i64]),
     "tread_topk_select_bf16": (c_int, [c_void, c_i64, c_i64, c_void, c_void, c_size, c_void]),
+    "tread_subset_attn_workspace_bytes": (c_size, [c_i64, c_int, c_int, c_int, c_i64]),
     "tread_subset_attn_bf16": (c_int, [c_void, c_void, c_void, c_void, c_void, c_i64, c_i64, c_int, c_int, c_int,
-                                       c_i64, c_float, c_void, c_void]),
+                                       c_i64, c_float, c_void, c_void, c_size, c_void]),
     "tread_add_rmsnorm_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_int, c_void, c_void, c_void]),
     "tread_silu_mul_bf16": (c_int, [c_void, c_i64, c_int, c_void, c_void]),
     "tread_copy_async": (c_int, [c_void, c_void, c_size, c_void, c_void]),
@@ -242,9 +243,12 @@ def subset_attn(q, k_cache, v_cache, kend, hq, hkv, hd, scale, kseg=None, n_shar
         raise ValueError(f"q has {q.numel()} elements, expected {n}x{hq}x{hd}")
     if out is None:
         out = torch.empty(n, hq * hd, dtype=q.dtype, device=q.device)
+    t_cap = k_cache.shape[-2]
+    wsb = lib().tread_subset_attn_workspace_bytes(n, hq, hkv, hd, t_cap)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=q.device) if wsb else None
     _check("tread_subset_attn_bf16", lib().tread_subset_attn_bf16(
         _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(kend), _ptr(kseg), int(n_shared), n, hq, hkv, hd,
-        k_cache.shape[-2], float(scale), _ptr(out), _stream()))
+        t_cap, float(scale), _ptr(out), _ptr(ws), wsb, _stream()))
     return out
 
 

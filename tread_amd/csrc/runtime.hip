@@ -34,7 +34,7 @@ int check_launch(const char* what) {
 
 extern "C" const char* tread_last_error(void) { return tread::g_err; }
 
-extern "C" int tread_abi_version(void) { return 1; }
+extern "C" int tread_abi_version(void) { return 2; }
 
 extern "C" int tread_copy_async(void* dst, const void* src, size_t bytes, tread_stream_t stream,
                                 tread_event_t done) {
