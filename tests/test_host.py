@@ -1,0 +1,137 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports every entry point
+include/tread_hip.h declares, the product refuses CPU tensors (no CPU fallback), and the engine's
+host logic (keys, sig, budgets, bucket plans) matches the reference's."""
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from oracle import tread_ref as R
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def header_functions():
+    text = (ROOT / "include" / "tread_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tread_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from tread_amd import _hip
+    lib = _hip.lib()  # raises if the library is missing or has a stale ABI
+    declared = header_functions()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert sorted(_hip.exported_symbols()) == declared
+    assert lib.tread_abi_version() == _hip.ABI_VERSION
+
+
+def test_library_symbols_in_dynamic_table():
+    import subprocess
+    so = ROOT / "tread_amd" / "libtread_hip.so"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(so)], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (tread_\w+)", out))
+    assert set(header_functions()) <= exported
+
+
+def test_error_paths_are_reported_without_a_gpu():
+    """Argument validation happens on the host before any launch: bad calls return an error code
+    and a message (no device touched)."""
+    import ctypes
+    from tread_amd import _hip
+    lib = _hip.lib()
+    rc = lib.tread_subset_attn_bf16(None, None, None, None, None, 0, 5, 28, 3, 128, 100, 0.1, None, None, 0, None)
+    assert rc != 0 and b"bad shape" in lib.tread_last_error()
+    rc = lib.tread_topk_select_bf16(None, 10, 11, None, None, 0, None)
+    assert rc != 0 and b"outside" in lib.tread_last_error()
+    rc = lib.tread_rope_assemble_bf16(None, 1, None, None, 2, 2, 10, 128, None, 0, 2, None)
+    assert rc != 0
+    assert lib.tread_topk_workspace_bytes(1000) == 0
+    # split-K workspace only for few rows over a long cache
+    assert lib.tread_subset_attn_workspace_bytes(32, 28, 4, 128, 32096) > 0
+    assert lib.tread_subset_attn_workspace_bytes(6400, 28, 4, 128, 32096) == 0
+
+
+def test_product_kernels_refuse_cpu_tensors():
+    from tread_amd import _hip
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        _hip.add_rmsnorm(x, torch.ones(64, dtype=torch.bfloat16), 1e-6)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        _hip.topk_select(torch.zeros(10, dtype=torch.bfloat16), 3)
+
+
+def test_engine_sig_matches_reference_form():
+    from tread_amd.engine import model_sig
+    from tread_amd.model import DecoderLM, preset
+    cfg = preset("qwen2.5-0.5b", num_hidden_layers=1, vocab_size=64, hidden_size=64, intermediate_size=64,
+                 num_attention_heads=2, num_key_value_heads=1)
+
+    class Shell:  # model_sig reads only config and dtype
+        config = cfg
+        dtype = torch.bfloat16
+    assert model_sig(Shell) == ("", "torch.bfloat16", 1000000.0, None) == R.sig_of(cfg, torch.bfloat16)
+
+
+def test_model_sig_reads_theta_from_rope_parameters():
+    """A transformers 5.x config keeps theta in rope_parameters; the key must still carry it."""
+    from transformers import Qwen2Config
+    from tread_amd.engine import model_sig
+    hc = Qwen2Config(hidden_size=64, num_attention_heads=2, num_key_value_heads=1, rope_theta=1000000.0)
+
+    class Shell:
+        config = hc
+        dtype = torch.bfloat16
+    sig = model_sig(Shell)
+    assert sig[1:] == ("torch.bfloat16", 1000000.0, None)
+
+
+def test_product_and_oracle_block_keys_agree():
+    from tread_amd.store import block_key
+    g = torch.Generator().manual_seed(0)
+    for n in (0, 1, 17, 1000):
+        ids = torch.randint(0, 152064, (n,), generator=g)
+        parts = ("", "torch.bfloat16", 1000000.0, None, "ns", "prefix", ids)
+        assert block_key(*parts) == R.block_key(*parts)
+        assert block_key("abc", ids) == R.block_key("abc", ids.to(torch.int32))
+
+
+def test_split_plan_and_graph_buckets():
+    from tread_amd.graphs import _bucket, _q_room
+    assert _bucket(6400, 32064) == (6400, 32768)  # the 7B 32k request at 20%
+    assert _bucket(16000, 32064) == (16128, 32768)
+    assert _bucket(1600, 8064) == (1792, 9216)
+    assert _q_room(32) == 256 and _q_room(300) == 512
+
+
+def test_synthetic_init_is_deterministic_and_shaped():
+    from tread_amd.model import ModelConfig, prepare, synthetic_model
+    cfg = ModelConfig(128, 64, 2, 4, 2, 16, 96)
+    a = synthetic_model(cfg, "cpu", torch.float32, seed=3, bias_std=0.1)
+    b = synthetic_model(cfg, "cpu", torch.float32, seed=3, bias_std=0.1)
+    for (na, pa), (_, pb) in zip(a.state_dict().items(), b.state_dict().items()):
+        assert torch.equal(pa, pb), na
+    P = prepare(a)
+    lw = P.layers[0]
+    assert lw.wqkv.shape == ((4 + 2 * 2) * 16, 64) and lw.wgu.shape == (192, 64)
+    assert lw.wqkv.data_ptr() == a.model.layers[0].self_attn.q_proj.weight.data_ptr()
+    sd = a.state_dict()
+    assert torch.equal(sd["model.layers.0.self_attn.k_proj.weight"], lw.wqkv[64:96])
+    assert torch.allclose(sd["model.layers.0.input_layernorm.weight"], torch.ones(64))
+    w = sd["model.layers.1.mlp.down_proj.weight"]
+    assert abs(w.std().item() - 0.02) < 0.004
+
+
+def test_prepare_fuses_a_transformers_model():
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    from tread_amd.model import prepare
+    hf = Qwen2ForCausalLM(Qwen2Config(vocab_size=64, hidden_size=32, num_hidden_layers=1, num_attention_heads=4,
+                                      num_key_value_heads=2, intermediate_size=48, rope_theta=1000000.0))
+    P = prepare(hf)
+    at = hf.model.layers[0].self_attn
+    assert torch.equal(P.layers[0].wqkv, torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight]))
+    assert torch.equal(P.inv_freq, hf.model.rotary_emb.inv_freq.float())
+    assert P.hd == 8 and P.hq == 4 and P.hkv == 2
