@@ -1,20 +1,21 @@
 // (a) Fused RoPE re-rotation + gather/append of cached KV blocks into the assembled cache.
 //
 // One streaming pass over HBM: every source row is read once and written once. A work unit is
-// (source, layer, kv head, chunk of ROWS token rows); within a unit the source rows and the
+// (source, layer, kv head, 16 token rows for hd 128); within a unit the source rows and the
 // destination rows are each one contiguous span, so K and V move as 16-byte vectors with
-// non-temporal loads and stores. K rows of a rotated source are processed as pairs of 16-byte
-// vectors (j, j + hd/2), the two halves that rotate_half mixes. cos/sin come from a per-source fp32
-// table (the caller builds it exactly as the reference's rotary embedding does) and are staged in LDS
-// while the work group's loads are in flight. The rotation keeps the reference's fp32 op order with
-// no contraction, fl(fl(x1*c) + fl(-x2*s)) and fl(fl(x2*c) + fl(x1*s)), then one RNE to bf16.
+// non-temporal loads and stores. Units are small and many (~10^5 per request) and each thread
+// issues all of its loads before its first store, the shape that reaches the copy ceiling. A
+// rotated K row is processed as pairs of 16-byte vectors (j, j + hd/2), the two halves that
+// rotate_half mixes, one pair per thread. cos/sin come from a per-source fp32 table (the caller
+// builds it exactly as the reference's rotary embedding does; 512 B per source, cache resident).
+// The rotation keeps the reference's fp32 op order with no contraction,
+// fl(fl(x1*c) + fl(-x2*s)) and fl(fl(x2*c) + fl(x1*s)), then one RNE to bf16.
 #include "common.h"
 #include "../../include/tread_hip.h"
 
 namespace tread {
 
 constexpr int ASM_MAX_SRC = 48;
-constexpr int ASM_ROWS = 128;
 constexpr int ASM_THREADS = 256;
 
 struct AsmSrc {
@@ -42,114 +43,104 @@ struct AsmArgs {
   int32_t pad;
 };
 
+// Rows per work unit: one 16-byte V chunk per thread; rotation pairs (8 + 8 K elements) on the
+// first half of the threads.
+template <int HD>
+constexpr int asm_rows() { return ASM_THREADS / (HD / 8); }
+
 template <int HD>
 __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArgs a) {
   constexpr int HALF = HD / 2;
-  constexpr int KPAIRS = ASM_ROWS * HALF / 8;  // (row, 8-wide column group of the first half)
-  constexpr int KP_PER_T = KPAIRS / ASM_THREADS;
-  constexpr int VCH = ASM_ROWS * HD / 8;  // 16-byte chunks per unit
-  constexpr int V_PER_T = VCH / ASM_THREADS;
-  __shared__ float s_cos[HALF];
-  __shared__ float s_sin[HALF];
+  constexpr int PG = HALF / 8;               // pair groups per K row
+  constexpr int ROWS = asm_rows<HD>();       // 16 (hd 128) or 32 (hd 64)
+  constexpr int V_PER_T = ROWS * (HD / 8) / ASM_THREADS;  // 16-byte chunks per thread: 1
 
   const int u = blockIdx.x;
   if (u >= a.total_units) return;
-  int s = 0;
-  while (s + 1 < a.n_src && u >= a.src[s + 1].unit_begin) ++s;
+  int lo = 0, hi = a.n_src - 1;  // last source whose first unit is <= u
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (a.src[mid].unit_begin <= u) lo = mid; else hi = mid - 1;
+  }
+  const int s = lo;
   const AsmSrc& src = a.src[s];
   const int local = u - src.unit_begin;
   const int chunk = local % src.chunks;
   const int lh = local / src.chunks;
   const int head = lh % a.n_kv;
   const int layer = a.layer_lo + lh / a.n_kv;
-  const int64_t row0 = (int64_t)chunk * ASM_ROWS;
-  const int rows = (int)min<int64_t>(ASM_ROWS, src.n - row0);
+  const int64_t row0 = (int64_t)chunk * ROWS;
+  const int rows = (int)min<int64_t>(ROWS, src.n - row0);
   const int64_t soff = (((int64_t)layer * a.n_kv + head) * src.n + row0) * HD;
   const int64_t doff = (((int64_t)layer * a.n_kv + head) * a.t_cap + src.dst_off + row0) * HD;
   const int tid = threadIdx.x;
-  const int nvec = rows * HD / 8;  // valid 16-byte chunks in this unit
+  const int nvec = rows * HD / 8;  // valid 16-byte chunks of this unit's K or V span
+  const u32x4_t* vs = reinterpret_cast<const u32x4_t*>(src.v + soff);
+  u32x4_t* vd = reinterpret_cast<u32x4_t*>(a.dv + doff);
 
-  // V: contiguous span copy.
-  {
-    const u32x4_t* vs = reinterpret_cast<const u32x4_t*>(src.v + soff);
-    u32x4_t* vd = reinterpret_cast<u32x4_t*>(a.dv + doff);
-    u32x4_t buf[V_PER_T];
+  if (src.delta == 0) {  // K and V are both bit copies of one contiguous span each
+    const u32x4_t* ks = reinterpret_cast<const u32x4_t*>(src.k + soff);
+    u32x4_t* kd = reinterpret_cast<u32x4_t*>(a.dk + doff);
+    u32x4_t vb[V_PER_T], kb[V_PER_T];
 #pragma unroll
     for (int j = 0; j < V_PER_T; ++j) {
       int c = tid + j * ASM_THREADS;
-      if (c < nvec) buf[j] = ldg_nt(vs + c);
-    }
-    if (src.delta == 0) {
-      // K is a bit copy as well: same span shape as V.
-      const u32x4_t* ks = reinterpret_cast<const u32x4_t*>(src.k + soff);
-      u32x4_t* kd = reinterpret_cast<u32x4_t*>(a.dk + doff);
-      u32x4_t kb[V_PER_T];
-#pragma unroll
-      for (int j = 0; j < V_PER_T; ++j) {
-        int c = tid + j * ASM_THREADS;
-        if (c < nvec) kb[j] = ldg_nt(ks + c);
+      if (c < nvec) {
+        vb[j] = ldg_nt(vs + c);
+        kb[j] = ldg_nt(ks + c);
       }
-#pragma unroll
-      for (int j = 0; j < V_PER_T; ++j) {
-        int c = tid + j * ASM_THREADS;
-        if (c < nvec) {
-          stg_nt(vd + c, buf[j]);
-          stg_nt(kd + c, kb[j]);
-        }
-      }
-      return;
     }
 #pragma unroll
     for (int j = 0; j < V_PER_T; ++j) {
       int c = tid + j * ASM_THREADS;
-      if (c < nvec) stg_nt(vd + c, buf[j]);
+      if (c < nvec) {
+        stg_nt(vd + c, vb[j]);
+        stg_nt(kd + c, kb[j]);
+      }
     }
+    return;
   }
 
-  // K with rotation by delta.
-  const bf16_t* ks = src.k + soff;
-  bf16_t* kd = a.dk + doff;
-  u32x4_t x1[KP_PER_T], x2[KP_PER_T];
+  // every load first: V chunks, the K pair, this column group's cos/sin
+  const int r = tid / PG, c = (tid % PG) * 8;
+  const bf16_t* kr = src.k + soff + (int64_t)r * HD;
+  u32x4_t vb[V_PER_T], x1, x2;
 #pragma unroll
-  for (int j = 0; j < KP_PER_T; ++j) {
-    int t = tid + j * ASM_THREADS;
-    int r = t / (HALF / 8);
-    int c = (t % (HALF / 8)) * 8;
-    if (r < rows) {
-      x1[j] = ldg_nt(reinterpret_cast<const u32x4_t*>(ks + (int64_t)r * HD + c));
-      x2[j] = ldg_nt(reinterpret_cast<const u32x4_t*>(ks + (int64_t)r * HD + c + HALF));
-    }
+  for (int j = 0; j < V_PER_T; ++j) {
+    int cc = tid + j * ASM_THREADS;
+    if (cc < nvec) vb[j] = ldg_nt(vs + cc);
   }
-  if (tid < HALF) {
-    const float* cs = a.cos_sin + ((int64_t)s * HALF + tid) * 2;
-    s_cos[tid] = cs[0];
-    s_sin[tid] = cs[1];
+  if (r < rows) {
+    x1 = ldg_nt(reinterpret_cast<const u32x4_t*>(kr + c));
+    x2 = ldg_nt(reinterpret_cast<const u32x4_t*>(kr + c + HALF));
   }
-  __syncthreads();
+  const f32x4_t* tab = reinterpret_cast<const f32x4_t*>(a.cos_sin + ((int64_t)s * HALF + c) * 2);
+  f32x4_t t0 = tab[0], t1 = tab[1], t2 = tab[2], t3 = tab[3];  // (cos, sin) of columns c..c+7
 #pragma unroll
-  for (int j = 0; j < KP_PER_T; ++j) {
-    int t = tid + j * ASM_THREADS;
-    int r = t / (HALF / 8);
-    int c = (t % (HALF / 8)) * 8;
-    if (r < rows) {
-      u32x4_t o1, o2;
+  for (int j = 0; j < V_PER_T; ++j) {
+    int cc = tid + j * ASM_THREADS;
+    if (cc < nvec) stg_nt(vd + cc, vb[j]);
+  }
+  if (r < rows) {
+    const float cv[8] = {t0[0], t0[2], t1[0], t1[2], t2[0], t2[2], t3[0], t3[2]};
+    const float sv[8] = {t0[1], t0[3], t1[1], t1[3], t2[1], t2[3], t3[1], t3[3]};
+    u32x4_t o1, o2;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        float cl = s_cos[c + 2 * w], ch = s_cos[c + 2 * w + 1];
-        float sl = s_sin[c + 2 * w], sh = s_sin[c + 2 * w + 1];
-        float al = lo_bf(x1[j][w]), ah = hi_bf(x1[j][w]);
-        float bl = lo_bf(x2[j][w]), bh = hi_bf(x2[j][w]);
-        // first half: x1*cos + (-x2)*sin ; second half: x2*cos + x1*sin; each product and sum
-        // rounded to fp32 on its own, as the reference's separate torch ops do
-        {
+    for (int w = 0; w < 4; ++w) {
+      const float cl = cv[2 * w], ch = cv[2 * w + 1], sl = sv[2 * w], sh = sv[2 * w + 1];
+      const float al = lo_bf(x1[w]), ah = hi_bf(x1[w]);
+      const float bl = lo_bf(x2[w]), bh = hi_bf(x2[w]);
+      // first half: x1*cos + (-x2)*sin ; second half: x2*cos + x1*sin; each product and sum
+      // rounded to fp32 on its own, as the reference's separate torch ops do
+      {
 #pragma clang fp contract(off)
-          o1[w] = pack_bf(al * cl + (-bl) * sl, ah * ch + (-bh) * sh);
-          o2[w] = pack_bf(bl * cl + al * sl, bh * ch + ah * sh);
-        }
+        o1[w] = pack_bf(al * cl + (-bl) * sl, ah * ch + (-bh) * sh);
+        o2[w] = pack_bf(bl * cl + al * sl, bh * ch + ah * sh);
       }
-      stg_nt(reinterpret_cast<u32x4_t*>(kd + (int64_t)r * HD + c), o1);
-      stg_nt(reinterpret_cast<u32x4_t*>(kd + (int64_t)r * HD + c + HALF), o2);
     }
+    bf16_t* kd = a.dk + doff + (int64_t)r * HD;
+    stg_nt(reinterpret_cast<u32x4_t*>(kd + c), o1);
+    stg_nt(reinterpret_cast<u32x4_t*>(kd + c + HALF), o2);
   }
 }
 
@@ -192,7 +183,8 @@ extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void
       d.n = s.n_tokens;
       d.dst_off = s.dst_off;
       d.delta = (int32_t)s.delta;
-      d.chunks = (int32_t)((s.n_tokens + ASM_ROWS - 1) / ASM_ROWS);
+      const int rows_per_unit = head_dim == 128 ? asm_rows<128>() : asm_rows<64>();
+      d.chunks = (int32_t)((s.n_tokens + rows_per_unit - 1) / rows_per_unit);
       d.unit_begin = (int32_t)units;
       units += (int64_t)n_lr * n_kv * d.chunks;
     }
