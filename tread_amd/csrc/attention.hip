@@ -2,13 +2,15 @@
 //
 // Rows are (query token, query head) pairs of one KV head group: row r of KV head h is token
 // r / G, query head h*G + r % G (G = hq / hkv), so the G heads that share a KV head share every
-// K/V tile staged in LDS (GQA in-kernel, no repeat_kv). A work group of 4 waves owns 128 rows;
-// each wave owns 32 rows and computes the transposed score block S^T = K Q^T, so that after the
+// K/V tile staged in LDS (GQA in-kernel, no repeat_kv). A work group of 4 waves owns 256 rows;
+// each wave owns two 32-row query blocks (every K/V fragment it reads from LDS feeds both) and
+// computes the transposed score blocks S^T = K Q^T, so that after the
 // softmax its probabilities already sit in the B-operand layout of O^T = V^T P^T: every lane
 // holds one query column for both products, and the online-softmax rescale is a per-lane scalar.
-// K tiles are staged row-major [key][d]; V tiles are staged transposed [d][key] so the A operand
-// of the PV product is two 8-byte LDS reads per lane. Tiles are double-buffered in LDS with one
-// barrier per 64-key tile. The key range of a work group is the union of [0, n_shared) and
+// K and V tiles are staged row-major [key][d] in LDS; the A operand of the PV product (V^T) is
+// read with gfx950's transposing LDS read, two 8-byte reads per lane and fragment. Tiles are
+// double-buffered in LDS with one barrier per 64-key tile. The online softmax keeps a stale row
+// max until it is 2^8 too small, so the O rescale runs a handful of times per row, not per tile. The key range of a work group is the union of [0, n_shared) and
 // [min kseg, max kend]; the visibility predicate (key <= kend[row] and key outside the row's
 // masked gap) is evaluated in registers only on tiles that cross a row's boundary.
 //
@@ -26,8 +28,9 @@ namespace tread {
 
 constexpr int ATT_WAVES = 4;
 constexpr int ATT_THREADS = ATT_WAVES * 64;
-constexpr int ATT_BM = ATT_WAVES * 32;  // rows per work group
-constexpr int ATT_BK = 64;              // keys per tile
+constexpr int ATT_QB = 2;                      // 32-row query blocks per wave
+constexpr int ATT_BM = ATT_WAVES * 32 * ATT_QB;  // rows per work group
+constexpr int ATT_BK = 64;                     // keys per tile
 constexpr int N_XCD = 8;
 constexpr int ATT_TARGET_WGS = 512;     // split-K when fewer (head, row tile) work groups than this
 constexpr int ATT_MIN_SPLIT_KEYS = 1024;
@@ -54,12 +57,25 @@ struct AttnArgs {
 
 template <int HD>
 struct AttnSmem {
-  static constexpr int KSTR = HD + 8;      // Ks row stride (elements)
-  static constexpr int VSTR = ATT_BK + 4;  // VT row stride (elements)
+  // K rows padded by 16 B: a wave's 32 row-parallel 16-byte fragment reads spread over all banks.
+  static constexpr int KSTR = HD + 8;
+  // V rows padded by 64 B (stride = 16 banks mod 64): the transpose reads of a wave touch 8 rows
+  // x 64 contiguous bytes, which then fall on every bank exactly twice.
+  static constexpr int VSTR = HD + 32;
   static constexpr int K_ELEMS = ATT_BK * KSTR;
-  static constexpr int V_ELEMS = HD * VSTR;
+  static constexpr int V_ELEMS = ATT_BK * VSTR;
   static constexpr int BUF = K_ELEMS + V_ELEMS;
 };
+
+// Transposing LDS read (ds_read_b64_tr_b16): in each group of 16 lanes, lane i receives element
+// (i % 4) of the 8-byte chunks addressed by lanes 4k + i / 4, k = 0..3.
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4_t;
+__device__ __forceinline__ s16x4_t lds_read_tr16(const bf16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4_t*)((__attribute__((address_space(3))) char*)(uintptr_t)p));
+}
+
+constexpr float ATT_RESCALE_LOG2 = 8.0f;  // keep a stale row max until it is 2^8 too small
 
 __device__ __forceinline__ int wave_max(int v) {
 #pragma unroll
@@ -78,8 +94,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   constexpr int KS = HD / 16;   // k-steps of the QK product
   constexpr int DB = HD / 32;   // 32-row d blocks of O^T
   constexpr int KCH = HD / 8;   // 16-byte chunks per K/V row
-  constexpr int K_LD = ATT_BK * KCH / ATT_THREADS;  // K chunks per thread per tile
-  constexpr int KPT = HD / 32;  // keys per thread in the V transpose (4 or 2)
+  constexpr int K_LD = ATT_BK * KCH / ATT_THREADS;  // K (and V) chunks per thread per tile
   extern __shared__ __align__(16) bf16_t smem[];
   __shared__ int red[4][ATT_WAVES];
 
@@ -104,24 +119,36 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int c = lane & 31, half = lane >> 5;
   const int64_t R = a.n * a.G;
-  const int64_t r = (int64_t)tile * ATT_BM + wv * 32 + c;
-  const bool valid = r < R;
-  const int64_t qi = valid ? r / a.G : 0;
-  const int qh = head * a.G + (int)(valid ? r % a.G : 0);
-  int my_end = -1, my_seg = 0;
-  if (valid) {
-    int64_t e = a.kend[qi];
-    my_end = (int)min<int64_t>(max<int64_t>(e, -1), a.t_cap - 1);
-    if (a.kseg) my_seg = (int)min<int64_t>(max<int64_t>(a.kseg[qi], 0), a.t_cap);
-  }
   const int n_shared = a.kseg ? (int)min<int64_t>(a.n_shared, a.t_cap) : 0;
+  // this lane's query column in each of the wave's query blocks
+  bool valid[ATT_QB];
+  int64_t qi[ATT_QB];
+  int qh[ATT_QB], my_end[ATT_QB], my_seg[ATT_QB];
+  int vmax = -1, vmin = 0x7fffffff, smax = 0, smin = 0x7fffffff;
+#pragma unroll
+  for (int b = 0; b < ATT_QB; ++b) {
+    const int64_t r = (int64_t)tile * ATT_BM + (wv * ATT_QB + b) * 32 + c;
+    valid[b] = r < R;
+    qi[b] = valid[b] ? r / a.G : 0;
+    qh[b] = head * a.G + (int)(valid[b] ? r % a.G : 0);
+    my_end[b] = -1;
+    my_seg[b] = 0;
+    if (valid[b]) {
+      my_end[b] = (int)min<int64_t>(max<int64_t>(a.kend[qi[b]], -1), a.t_cap - 1);
+      if (a.kseg) my_seg[b] = (int)min<int64_t>(max<int64_t>(a.kseg[qi[b]], 0), a.t_cap);
+      vmax = max(vmax, my_end[b]);
+      vmin = min(vmin, my_end[b]);
+      smax = max(smax, my_seg[b]);
+      smin = min(smin, my_seg[b]);
+    }
+  }
 
   // ---- work-group key range
   {
-    int vmax = wave_max(my_end);
-    int vmin = wave_min(valid ? my_end : 0x7fffffff);
-    int smax = wave_max(valid ? my_seg : 0);
-    int smin = wave_min(valid ? my_seg : 0x7fffffff);
+    vmax = wave_max(vmax);
+    vmin = wave_min(vmin);
+    smax = wave_max(smax);
+    smin = wave_min(smin);
     if (lane == 0) {
       red[0][wv] = vmax;
       red[1][wv] = vmin;
@@ -152,22 +179,25 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   const int ntiles = nA + nB;
 
   // ---- Q^T fragments (B operand), resident for the whole kernel
-  bf16x8_t qf[KS];
-  {
-    const bf16_t* qp = a.q + (qi * a.hq + qh) * HD + half * 8;
+  bf16x8_t qf[ATT_QB][KS];
+#pragma unroll
+  for (int b = 0; b < ATT_QB; ++b) {
+    const bf16_t* qp = a.q + (qi[b] * a.hq + qh[b]) * HD + half * 8;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       u32x4_t t = {0, 0, 0, 0};
-      if (valid) t = *reinterpret_cast<const u32x4_t*>(qp + s * 16);
-      qf[s] = __builtin_bit_cast(bf16x8_t, t);
+      if (valid[b]) t = *reinterpret_cast<const u32x4_t*>(qp + s * 16);
+      qf[b][s] = __builtin_bit_cast(bf16x8_t, t);
     }
   }
 
   const bf16_t* kbase = a.k + (int64_t)head * a.t_cap * HD;
   const bf16_t* vbase = a.v + (int64_t)head * a.t_cap * HD;
-  const int vdg = tid % KCH, vkg = tid / KCH;  // V transpose: d group, key group
+  // this lane's part of a V^T fragment read: rows (keys) and column (d) offsets, see lds_read_tr16
+  const int tr_g = lane >> 4, tr_j = lane & 15;
+  const int tr_off = (half * 4 + (tr_j >> 2)) * SM::VSTR + (tr_g & 1) * 16 + (tr_j & 3) * 4;
 
-  u32x4_t kreg[K_LD], vreg[KPT];
+  u32x4_t kreg[K_LD], vreg[K_LD];
   auto tile_bounds = [&](int j, int& s0, int& s1) {
     if (j < nA) {
       s0 = startA + j * ATT_BK;
@@ -189,45 +219,40 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       kreg[x] = t;
     }
 #pragma unroll
-    for (int x = 0; x < KPT; ++x) {
-      int key = vkg * KPT + x;
+    for (int x = 0; x < K_LD; ++x) {
+      int ch = tid + x * ATT_THREADS;
+      int key = ch / KCH, cc = ch % KCH;
       u32x4_t t = {0, 0, 0, 0};
-      if (s0 + key < s1) t = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)(s0 + key) * HD + vdg * 8);
+      if (s0 + key < s1) t = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)(s0 + key) * HD + cc * 8);
       vreg[x] = t;
     }
   };
   auto lstore = [&](int buf) {
     bf16_t* Ks = smem + buf * SM::BUF;
-    bf16_t* VT = Ks + SM::K_ELEMS;
+    bf16_t* Vs = Ks + SM::K_ELEMS;
 #pragma unroll
     for (int x = 0; x < K_LD; ++x) {
       int ch = tid + x * ATT_THREADS;
       int key = ch / KCH, cc = ch % KCH;
       *reinterpret_cast<u32x4_t*>(Ks + key * SM::KSTR + cc * 8) = kreg[x];
-    }
-    // transpose: element e of key (vkg*KPT + x) goes to VT[vdg*8 + e][vkg*KPT + x]
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      uint32_t w[KPT];
-#pragma unroll
-      for (int x = 0; x < KPT; ++x) w[x] = (e & 1) ? (vreg[x][e >> 1] >> 16) : (vreg[x][e >> 1] & 0xffffu);
-      bf16_t* dst = VT + (vdg * 8 + e) * SM::VSTR + vkg * KPT;
-      if constexpr (KPT == 4) {
-        u32x2_t pk = {w[0] | (w[1] << 16), w[2] | (w[3] << 16)};
-        *reinterpret_cast<u32x2_t*>(dst) = pk;
-      } else {
-        *reinterpret_cast<uint32_t*>(dst) = w[0] | (w[1] << 16);
-      }
+      *reinterpret_cast<u32x4_t*>(Vs + key * SM::VSTR + cc * 8) = vreg[x];
     }
   };
 
-  f32x16_t oacc[DB];
+  f32x16_t oacc[ATT_QB][DB];
 #pragma unroll
-  for (int d = 0; d < DB; ++d)
+  for (int b = 0; b < ATT_QB; ++b)
 #pragma unroll
-    for (int x = 0; x < 16; ++x) oacc[d][x] = 0.f;
-  // running max (log2-scaled units) and sum of this lane's query row
-  float m_run = -1e30f, l_run = 0.f;
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) oacc[b][d][x] = 0.f;
+  // running max (log2-scaled units) and sum of this lane's query rows
+  float m_run[ATT_QB], l_run[ATT_QB];
+#pragma unroll
+  for (int b = 0; b < ATT_QB; ++b) {
+    m_run[b] = -1e30f;
+    l_run[b] = 0.f;
+  }
   const float cs = a.scale_log2;
 
   if (ntiles > 0) {
@@ -239,112 +264,126 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     __syncthreads();
     if (j + 1 < ntiles) gload(j + 1);
     const bf16_t* Ks = smem + buf * SM::BUF;
-    const bf16_t* VT = Ks + SM::K_ELEMS;
+    const bf16_t* Vs = Ks + SM::K_ELEMS;
     int s0, s1;
     tile_bounds(j, s0, s1);
 
-    // S^T = K Q^T for two 32-key blocks (raw, unscaled scores)
-    f32x16_t sacc[2];
+    const bool full = (s1 - s0 == ATT_BK) && (s1 - 1 <= kmin) && (j < nA || s0 >= segmax);
+    // each 32-key half of the tile: S^T = K Q^T for every query block (a K fragment read from
+    // LDS feeds them all), online softmax, then O^T += V^T P^T for those 32 keys
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
+      f32x16_t sacc[ATT_QB];
 #pragma unroll
-      for (int x = 0; x < 16; ++x) sacc[kb][x] = 0.f;
-      const bf16_t* kr = Ks + (kb * 32 + c) * SM::KSTR + half * 8;
+      for (int b = 0; b < ATT_QB; ++b)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) sacc[b][x] = 0.f;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(kr + s * 16);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[s], sacc[kb], 0, 0, 0);
-      }
-    }
-    // mask, row max (raw scores; the scale is positive so it commutes with max)
-    const bool full = (s1 - s0 == ATT_BK) && (s1 - 1 <= kmin) && (j < nA || s0 >= segmax);
-    if (!full) {
+        const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(Ks + (kb * 32 + c) * SM::KSTR + half * 8 + s * 16);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int b = 0; b < ATT_QB; ++b)
+          sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[b][s], sacc[b], 0, 0, 0);
+      }
+#pragma unroll
+      for (int b = 0; b < ATT_QB; ++b) {
+        if (!full) {
+#pragma unroll
+          for (int x = 0; x < 16; ++x) {
+            int key = s0 + kb * 32 + (x >> 2) * 8 + half * 4 + (x & 3);
+            bool vis = key < s1 && key <= my_end[b] && (key < n_shared || key >= my_seg[b]);
+            sacc[b][x] = vis ? sacc[b][x] : -INFINITY;
+          }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int x = 0; x < 16; ++x) tmax = fmaxf(tmax, sacc[b][x]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        // Lazy rescale: exponentiate against a stale row max m_run and move it (rescaling the
+        // running sum and O) only when some row's max outgrew it by more than 2^8; p then stays
+        // <= 256, and the final division by the sum is exact either way.
+        const float m_cand = fmaxf(m_run[b], tmax * cs);
+        if (__ballot(m_cand > m_run[b] + ATT_RESCALE_LOG2)) {
+          const float corr = __builtin_amdgcn_exp2f(m_run[b] - m_cand);
+          l_run[b] *= corr;
+#pragma unroll
+          for (int d = 0; d < DB; ++d)
+#pragma unroll
+            for (int x = 0; x < 16; ++x) oacc[b][d][x] *= corr;
+          m_run[b] = m_cand;
+        }
+        const float m_use = m_run[b];
+        float rs = 0.f;
 #pragma unroll
         for (int x = 0; x < 16; ++x) {
-          int key = s0 + kb * 32 + (x >> 2) * 8 + half * 4 + (x & 3);
-          bool vis = key < s1 && key <= my_end && (key < n_shared || key >= my_seg);
-          sacc[kb][x] = vis ? sacc[kb][x] : -INFINITY;
+          float p = __builtin_amdgcn_exp2f(fmaf(sacc[b][x], cs, -m_use));
+          sacc[b][x] = p;
+          rs += p;
         }
-    }
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int x = 0; x < 16; ++x) tmax = fmaxf(tmax, sacc[kb][x]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax * cs);
-    // rescale the running sum and O only if some row's max moved (rare after the first tiles)
-    if (__ballot(m_new > m_run)) {
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= corr;
-#pragma unroll
-      for (int d = 0; d < DB; ++d)
-#pragma unroll
-        for (int x = 0; x < 16; ++x) oacc[d][x] *= corr;
-    }
-    m_run = m_new;
-    float rs = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][x], cs, -m_new));
-        sacc[kb][x] = p;
-        rs += p;
+        rs += __shfl_xor(rs, 32);
+        l_run[b] += rs;
       }
-    rs += __shfl_xor(rs, 32);
-    l_run += rs;
-
-    // O^T += V^T P^T over 4 k-steps of 16 keys
+      // O^T += V^T P^T over the 2 k-steps (16 keys each) of this half; each V fragment feeds
+      // every query block
 #pragma unroll
-    for (int s = 0; s < ATT_BK / 16; ++s) {
-      const int kb = s >> 1, base = (s & 1) * 8;
-      u32x4_t pw;
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int s = kb * 2 + h2, base = h2 * 8;
+        bf16x8_t pb[ATT_QB];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) pw[q] = pack_bf(sacc[kb][base + 2 * q], sacc[kb][base + 2 * q + 1]);
-      const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, pw);
+        for (int b = 0; b < ATT_QB; ++b) {
+          u32x4_t pw;
 #pragma unroll
-      for (int d = 0; d < DB; ++d) {
-        const bf16_t* vr = VT + (d * 32 + c) * SM::VSTR + s * 16 + half * 4;
-        u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
-        u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 8);
-        u32x4_t av = {lo[0], lo[1], hi[0], hi[1]};
-        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, av), pb, oacc[d], 0, 0, 0);
+          for (int q = 0; q < 4; ++q) pw[q] = pack_bf(sacc[b][base + 2 * q], sacc[b][base + 2 * q + 1]);
+          pb[b] = __builtin_bit_cast(bf16x8_t, pw);
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+          // V^T fragment: keys s*16 + half*4 + (0..3) and s*16 + 8 + half*4 + (0..3) of column
+          // d*32 + lane%32, transposed on the fly out of the row-major V tile
+          const bf16_t* vr = Vs + tr_off + s * 16 * SM::VSTR + d * 32;
+          const s16x4_t lo = lds_read_tr16(vr);
+          const s16x4_t hi = lds_read_tr16(vr + 8 * SM::VSTR);
+          const bf16x8_t va = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+          for (int b = 0; b < ATT_QB; ++b)
+            oacc[b][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[b], oacc[b][d], 0, 0, 0);
+        }
       }
     }
     if (j + 1 < ntiles) lstore(buf ^ 1);
   }
 
-  if (!valid) return;
-  if (a.nsplit > 1) {
-    // partial for the combine kernel: unnormalised O, running max and sum
-    const int64_t p = (((int64_t)split * a.hkv + head) * a.tiles + tile) * ATT_BM + wv * 32 + c;
-    float* po = a.ws_o + p * HD;
+#pragma unroll
+  for (int b = 0; b < ATT_QB; ++b) {
+    if (!valid[b]) continue;
+    if (a.nsplit > 1) {
+      // partial for the combine kernel: unnormalised O, running max and sum
+      const int64_t p = (((int64_t)split * a.hkv + head) * a.tiles + tile) * ATT_BM + (wv * ATT_QB + b) * 32 + c;
+      float* po = a.ws_o + p * HD;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          f32x4_t o = {oacc[b][d][g4 * 4 + 0], oacc[b][d][g4 * 4 + 1], oacc[b][d][g4 * 4 + 2], oacc[b][d][g4 * 4 + 3]};
+          *reinterpret_cast<f32x4_t*>(po + d * 32 + g4 * 8 + half * 4) = o;
+        }
+      if (half == 0) {
+        a.ws_ml[p * 2] = m_run[b];
+        a.ws_ml[p * 2 + 1] = l_run[b];
+      }
+      continue;
+    }
+    const float inv = l_run[b] > 0.f ? 1.0f / l_run[b] : 0.f;
+    bf16_t* op = a.out + (qi[b] * a.hq + qh[b]) * HD;
 #pragma unroll
     for (int d = 0; d < DB; ++d)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        f32x4_t o = {oacc[d][g4 * 4 + 0], oacc[d][g4 * 4 + 1], oacc[d][g4 * 4 + 2], oacc[d][g4 * 4 + 3]};
-        *reinterpret_cast<f32x4_t*>(po + d * 32 + g4 * 8 + half * 4) = o;
+        u32x2_t o = {pack_bf(oacc[b][d][g4 * 4 + 0] * inv, oacc[b][d][g4 * 4 + 1] * inv),
+                     pack_bf(oacc[b][d][g4 * 4 + 2] * inv, oacc[b][d][g4 * 4 + 3] * inv)};
+        *reinterpret_cast<u32x2_t*>(op + d * 32 + g4 * 8 + half * 4) = o;
       }
-    if (half == 0) {
-      a.ws_ml[p * 2] = m_run;
-      a.ws_ml[p * 2 + 1] = l_run;
-    }
-    return;
   }
-  const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
-  bf16_t* op = a.out + (qi * a.hq + qh) * HD;
-#pragma unroll
-  for (int d = 0; d < DB; ++d)
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      u32x2_t o = {pack_bf(oacc[d][g4 * 4 + 0] * inv, oacc[d][g4 * 4 + 1] * inv),
-                   pack_bf(oacc[d][g4 * 4 + 2] * inv, oacc[d][g4 * 4 + 3] * inv)};
-      *reinterpret_cast<u32x2_t*>(op + d * 32 + g4 * 8 + half * 4) = o;
-    }
 }
 
 // Merge split-K partials: one wave per (kv head, row); each lane owns HD/64 output elements.
