@@ -2,13 +2,14 @@
 //
 // Rows are (query token, query head) pairs of one KV head group: row r of KV head h is token
 // r / G, query head h*G + r % G (G = hq / hkv), so the G heads that share a KV head share every
-// K/V tile staged in LDS (GQA in-kernel, no repeat_kv). A work group of 4 waves owns 256 rows;
-// each wave owns two 32-row query blocks (every K/V fragment it reads from LDS feeds both) and
-// computes the transposed score blocks S^T = K Q^T, so that after the
+// K/V tile staged in LDS (GQA in-kernel, no repeat_kv). A work group of 8 waves owns 256 rows
+// (ATT_QB 32-row query blocks per wave; one fits the register file best, 198 VGPRs and two waves
+// per SIMD) and each wave computes the transposed score blocks S^T = K Q^T, so that after the
 // softmax its probabilities already sit in the B-operand layout of O^T = V^T P^T: every lane
 // holds one query column for both products, and the online-softmax rescale is a per-lane scalar.
-// K and V tiles are staged row-major [key][d] in LDS; the A operand of the PV product (V^T) is
-// read with gfx950's transposing LDS read, two 8-byte reads per lane and fragment. Tiles are
+// K and V tiles go from global memory straight into LDS (no register staging), row-major
+// [key][d] with XOR-swizzled chunks; the A operand of the PV product (V^T) is read with gfx950's
+// transposing LDS read, two 8-byte reads per lane and fragment. Tiles are
 // double-buffered in LDS with one barrier per 64-key tile. The online softmax keeps a stale row
 // max until it is 2^8 too small, so the O rescale runs a handful of times per row, not per tile. The key range of a work group is the union of [0, n_shared) and
 // [min kseg, max kend]; the visibility predicate (key <= kend[row] and key outside the row's
@@ -26,9 +27,9 @@
 
 namespace tread {
 
-constexpr int ATT_WAVES = 4;
+constexpr int ATT_WAVES = 8;
 constexpr int ATT_THREADS = ATT_WAVES * 64;
-constexpr int ATT_QB = 2;                      // 32-row query blocks per wave
+constexpr int ATT_QB = 1;                      // 32-row query blocks per wave
 constexpr int ATT_BM = ATT_WAVES * 32 * ATT_QB;  // rows per work group
 constexpr int ATT_BK = 64;                     // keys per tile
 constexpr int N_XCD = 8;
@@ -55,16 +56,23 @@ struct AttnArgs {
   float scale_log2;
 };
 
+// K and V tiles live in LDS as unpadded [key][hd] rows of 16-byte chunks, filled straight from
+// global memory (global_load_lds_dwordx4: a wave's 64 x 16 B land contiguously). Bank conflicts
+// are avoided by XOR-swizzling the chunk index within a row instead of padding:
+//  - K: chunk j of row r sits at j ^ (r % NCH). A wave's A-operand reads take the same chunk of 32
+//    consecutive rows, which then spread over every bank;
+//  - V: chunk j of row r sits at j ^ fV(r), fV moving the chunk's upper bits with the low row
+//    bits, so a transposing read (8 rows x 64 contiguous bytes per wave) hits each bank twice.
 template <int HD>
 struct AttnSmem {
-  // K rows padded by 16 B: a wave's 32 row-parallel 16-byte fragment reads spread over all banks.
-  static constexpr int KSTR = HD + 8;
-  // V rows padded by 64 B (stride = 16 banks mod 64): the transpose reads of a wave touch 8 rows
-  // x 64 contiguous bytes, which then fall on every bank exactly twice.
-  static constexpr int VSTR = HD + 32;
-  static constexpr int K_ELEMS = ATT_BK * KSTR;
-  static constexpr int V_ELEMS = ATT_BK * VSTR;
+  static constexpr int NCH = HD / 8;  // 16-byte chunks per row
+  static constexpr int K_ELEMS = ATT_BK * HD;
+  static constexpr int V_ELEMS = ATT_BK * HD;
   static constexpr int BUF = K_ELEMS + V_ELEMS;
+  static __device__ __forceinline__ int k_swz(int r) { return r & (NCH - 1); }
+  static __device__ __forceinline__ int v_swz(int r) {
+    return HD == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2);
+  }
 };
 
 // Transposing LDS read (ds_read_b64_tr_b16): in each group of 16 lanes, lane i receives element
@@ -73,6 +81,12 @@ typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4_t;
 __device__ __forceinline__ s16x4_t lds_read_tr16(const bf16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) s16x4_t*)((__attribute__((address_space(3))) char*)(uintptr_t)p));
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land at lds + 16 l
+// (lds is wave-uniform).
+__device__ __forceinline__ void lds_load16(const bf16_t* g, bf16_t* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(uintptr_t)lds, 16, 0, 0);
 }
 
 constexpr float ATT_RESCALE_LOG2 = 8.0f;  // keep a stale row max until it is 2^8 too small
@@ -94,7 +108,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   constexpr int KS = HD / 16;   // k-steps of the QK product
   constexpr int DB = HD / 32;   // 32-row d blocks of O^T
   constexpr int KCH = HD / 8;   // 16-byte chunks per K/V row
-  constexpr int K_LD = ATT_BK * KCH / ATT_THREADS;  // K (and V) chunks per thread per tile
+  constexpr int K_LD = ATT_BK * KCH / ATT_THREADS;  // K (and V) 16-byte chunks per thread per tile
   extern __shared__ __align__(16) bf16_t smem[];
   __shared__ int red[4][ATT_WAVES];
 
@@ -193,11 +207,13 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
 
   const bf16_t* kbase = a.k + (int64_t)head * a.t_cap * HD;
   const bf16_t* vbase = a.v + (int64_t)head * a.t_cap * HD;
-  // this lane's part of a V^T fragment read: rows (keys) and column (d) offsets, see lds_read_tr16
+  // this lane's part of a V^T fragment read (see lds_read_tr16): tile row (key) offset, and the
+  // column (d) offset within a 32-wide d block
   const int tr_g = lane >> 4, tr_j = lane & 15;
-  const int tr_off = (half * 4 + (tr_j >> 2)) * SM::VSTR + (tr_g & 1) * 16 + (tr_j & 3) * 4;
+  const int tr_row = half * 4 + (tr_j >> 2);
+  const int tr_col = (tr_g & 1) * 16 + (tr_j & 3) * 4;
+  const int tr_swz = SM::v_swz(tr_row);  // equal for every row this lane reads (rows differ by multiples of 8)
 
-  u32x4_t kreg[K_LD], vreg[K_LD];
   auto tile_bounds = [&](int j, int& s0, int& s1) {
     if (j < nA) {
       s0 = startA + j * ATT_BK;
@@ -207,35 +223,23 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       s1 = min(s0 + ATT_BK, endB);
     }
   };
-  auto gload = [&](int j) {
+  // Queue the tile's K and V rows straight into LDS buffer `buf`. Load x of this wave fills LDS
+  // chunk positions [(x * ATT_WAVES + wv) * 64, +64), lane l position +l; the lane fetches the
+  // global chunk that the swizzle places there. Rows past the tile's end re-read its last row
+  // (finite data; those keys are masked), so nothing outside the cache is touched.
+  auto issue_tile = [&](int j, int buf) {
     int s0, s1;
     tile_bounds(j, s0, s1);
-#pragma unroll
-    for (int x = 0; x < K_LD; ++x) {
-      int ch = tid + x * ATT_THREADS;
-      int key = ch / KCH, cc = ch % KCH;
-      u32x4_t t = {0, 0, 0, 0};
-      if (s0 + key < s1) t = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)(s0 + key) * HD + cc * 8);
-      kreg[x] = t;
-    }
-#pragma unroll
-    for (int x = 0; x < K_LD; ++x) {
-      int ch = tid + x * ATT_THREADS;
-      int key = ch / KCH, cc = ch % KCH;
-      u32x4_t t = {0, 0, 0, 0};
-      if (s0 + key < s1) t = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)(s0 + key) * HD + cc * 8);
-      vreg[x] = t;
-    }
-  };
-  auto lstore = [&](int buf) {
     bf16_t* Ks = smem + buf * SM::BUF;
     bf16_t* Vs = Ks + SM::K_ELEMS;
 #pragma unroll
     for (int x = 0; x < K_LD; ++x) {
-      int ch = tid + x * ATT_THREADS;
-      int key = ch / KCH, cc = ch % KCH;
-      *reinterpret_cast<u32x4_t*>(Ks + key * SM::KSTR + cc * 8) = kreg[x];
-      *reinterpret_cast<u32x4_t*>(Vs + key * SM::VSTR + cc * 8) = vreg[x];
+      const int base = (x * ATT_WAVES + wv) * 64;  // first chunk position of this wave-wide load
+      const int pos = base + lane;
+      const int r = pos / KCH, p = pos % KCH;
+      const int64_t grow = min(s0 + r, s1 - 1);
+      lds_load16(kbase + grow * HD + (p ^ SM::k_swz(r)) * 8, Ks + base * 8);
+      lds_load16(vbase + grow * HD + (p ^ SM::v_swz(r)) * 8, Vs + base * 8);
     }
   };
 
@@ -255,14 +259,14 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   }
   const float cs = a.scale_log2;
 
-  if (ntiles > 0) {
-    gload(0);
-    lstore(0);
-  }
+  if (ntiles > 0) issue_tile(0, 0);
   for (int j = 0; j < ntiles; ++j) {
     const int buf = j & 1;
+    // tile j's LDS loads (this wave's) have landed; the barrier makes every wave's visible and
+    // guarantees nobody still reads buffer buf ^ 1 (tile j - 1), which the next loads overwrite
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (j + 1 < ntiles) gload(j + 1);
+    if (j + 1 < ntiles) issue_tile(j + 1, buf ^ 1);
     const bf16_t* Ks = smem + buf * SM::BUF;
     const bf16_t* Vs = Ks + SM::K_ELEMS;
     int s0, s1;
@@ -280,7 +284,8 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
         for (int x = 0; x < 16; ++x) sacc[b][x] = 0.f;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(Ks + (kb * 32 + c) * SM::KSTR + half * 8 + s * 16);
+        const int kr = kb * 32 + c;
+        const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(Ks + kr * HD + ((2 * s + half) ^ SM::k_swz(kr)) * 8);
 #pragma unroll
         for (int b = 0; b < ATT_QB; ++b)
           sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[b][s], sacc[b], 0, 0, 0);
@@ -340,9 +345,10 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
         for (int d = 0; d < DB; ++d) {
           // V^T fragment: keys s*16 + half*4 + (0..3) and s*16 + 8 + half*4 + (0..3) of column
           // d*32 + lane%32, transposed on the fly out of the row-major V tile
-          const bf16_t* vr = Vs + tr_off + s * 16 * SM::VSTR + d * 32;
+          const int col = d * 32 + tr_col;
+          const bf16_t* vr = Vs + (s * 16 + tr_row) * HD + (((col >> 3) ^ tr_swz) << 3) + (col & 7);
           const s16x4_t lo = lds_read_tr16(vr);
-          const s16x4_t hi = lds_read_tr16(vr + 8 * SM::VSTR);
+          const s16x4_t hi = lds_read_tr16(vr + 8 * HD);
           const bf16x8_t va = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
           for (int b = 0; b < ATT_QB; ++b)
@@ -350,7 +356,6 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
         }
       }
     }
-    if (j + 1 < ntiles) lstore(buf ^ 1);
   }
 
 #pragma unroll
