@@ -172,6 +172,11 @@ def main():
     ap.add_argument("--full-reps", type=int, default=3, help="full-prefill reps for the TTFT denominator (0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-tune", action="store_true",
+                    help="library-default GEMM solutions (default: the measured per-shape table in "
+                         "tread_amd/tuning, applied through PyTorch TunableOp)")
+    ap.add_argument("--retune", default=None, metavar="OUT_CSV",
+                    help="benchmark GEMM solutions for every shape met (warm-up absorbs it) and write them here")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}); "
@@ -181,6 +186,9 @@ def main():
     from tread_amd import BlockStore, Engine, prefill_full
     from tread_amd.model import preset, synthetic_model
 
+    if not args.no_tune:
+        from tread_amd.tuning import TABLE_7B, use_tuned_gemms
+        use_tuned_gemms(tables=() if args.retune else (TABLE_7B,), tune=bool(args.retune), out_file=args.retune)
     preset_name, n_docs, doc_len, n_sys, n_query = WORKLOADS[args.workload]
     cfg = preset(preset_name)
     dev = "cuda:0"
@@ -239,7 +247,8 @@ def main():
         "data": "synthetic (uniform random token ids, random-init N(0,0.02) weights)",
         "config": {"workload": args.workload, "model": preset_name, "context_tokens": T, "docs": n_docs,
                    "doc_len": doc_len, "system": n_sys, "query": n_query, "recompute_ratio": args.ratio,
-                   "policy": "deviation", "hipgraph": not args.eager, "parallelism": "single GPU"},
+                   "policy": "deviation", "hipgraph": not args.eager, "gemm_tuning": not args.no_tune,
+                   "parallelism": "single GPU"},
         "stages_ms": med,
         "ttft_full_prefill_ms": None if full_ms is None else round(full_ms, 2),
         "speedup_vs_full_prefill": None if full_ms is None else round(full_ms / ttft_ms, 2),
