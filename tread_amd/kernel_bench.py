@@ -1,0 +1,112 @@
+"""Kernel micro-benchmarks on synthetic inputs of the reuse workloads' shapes.
+
+    python -m tread_amd.kernel_bench assemble  [--workload qwen2.5-7b-32k] [--iters 20]
+    python -m tread_amd.kernel_bench attention [--workload qwen2.5-7b-32k] [--shape recompute|prefill|query]
+    python -m tread_amd.kernel_bench copy      [--workload qwen2.5-7b-32k]
+
+`assemble` launches the fused re-rotate+assemble kernel on one request's blocks (prefix + every
+doc, each doc shifted); `copy` copies the same number of bytes with torch (the calibration for
+HBM traffic counters); `attention` runs the recompute attention kernel on a recompute-shaped row
+set (20% of the doc positions, sorted), a full causal prefill, or the query rows. Each prints its
+time per launch and achieved GB/s or TFLOP/s; under rocprofv3 every launch is one dispatch.
+"""
+import argparse
+import sys
+
+import torch
+
+from tread_amd import _hip
+from tread_amd.model import inv_freq_of, preset
+
+WORKLOADS = {
+    "qwen2.5-7b-32k": ("qwen2.5-7b", 32, 1000, 64, 32),
+    "qwen2.5-1.5b-16k": ("qwen2.5-1.5b", 16, 1000, 64, 32),
+    "qwen2.5-0.5b-8k": ("qwen2.5-0.5b", 8, 1000, 64, 32),
+    "llama3-70b-32k": ("llama3-70b", 32, 1000, 64, 32),
+}
+
+
+def _timed(fn, iters):
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / iters
+
+
+def bench_assemble(cfg, n_docs, doc_len, n_sys, n_query, iters):
+    L, kv, hd = cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim
+    mk = lambda n: torch.randn(L, 1, kv, n, hd, device="cuda", dtype=torch.bfloat16)
+    srcs = [(mk(n_sys), mk(n_sys), 0, 0)]
+    for i in range(n_docs):  # doc i cached at base n_sys, placed at a permuted slot
+        off = n_sys + ((i * 7) % n_docs) * doc_len
+        srcs.append((mk(doc_len), mk(doc_len), off, off - n_sys))
+    T = n_sys + n_docs * doc_len
+    K = torch.empty(L, 1, kv, T + n_query, hd, device="cuda", dtype=torch.bfloat16)
+    V = torch.empty_like(K)
+    table = _hip.rope_assemble(srcs, K, V, inv_freq_of(cfg))
+    sec = _timed(lambda: _hip.rope_assemble(srcs, K, V, inv_freq_of(cfg), table=table), iters)
+    nbytes = 4 * T * L * kv * hd * 2
+    print(f"assemble: {sec * 1e6:.1f} us per launch, {nbytes} algorithmic bytes, {nbytes / sec / 1e9:.0f} GB/s")
+
+
+def bench_copy(cfg, n_docs, doc_len, n_sys, n_query, iters):
+    L, kv, hd = cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim
+    n = 2 * (n_sys + n_docs * doc_len) * L * kv * hd  # the assembled K + V element count
+    src = torch.empty(n, device="cuda", dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    sec = _timed(lambda: dst.copy_(src), iters)
+    print(f"copy: {n * 2} bytes read + written, {sec * 1e6:.1f} us, {2 * n * 2 / sec / 1e9:.0f} GB/s")
+
+
+def bench_attention(cfg, n_docs, doc_len, n_sys, n_query, iters, shape, ratio=0.2):
+    hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    T = n_sys + n_docs * doc_len
+    g = torch.Generator().manual_seed(0)
+    if shape == "recompute":
+        n = int(round(ratio * n_docs * doc_len))
+        kend = torch.sort(torch.randperm(n_docs * doc_len, generator=g)[:n]).values + n_sys
+        t_cap = T
+    elif shape == "prefill":
+        kend = torch.arange(T + n_query)
+        t_cap = T + n_query
+    else:
+        kend = torch.arange(T, T + n_query)
+        t_cap = T + n_query
+    n = kend.numel()
+    kend = kend.cuda()
+    q = torch.randn(n, hq, hd, device="cuda", dtype=torch.bfloat16)
+    K = torch.randn(1, hkv, t_cap, hd, device="cuda", dtype=torch.bfloat16)
+    V = torch.randn_like(K)
+    out = torch.empty(n, hq * hd, device="cuda", dtype=torch.bfloat16)
+    sec = _timed(lambda: _hip.subset_attn(q, K, V, kend, hq, hkv, hd, hd ** -0.5, out=out), iters)
+    flop = 4 * hq * hd * (kend + 1).double().sum().item()
+    print(f"attention[{shape}]: rows {n} x {hq} heads over <= {t_cap} keys: {sec * 1e3:.3f} ms, "
+          f"{flop / sec / 1e12:.1f} TFLOP/s")
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("kernel", choices=["assemble", "copy", "attention"])
+    ap.add_argument("--workload", default="qwen2.5-7b-32k", choices=list(WORKLOADS))
+    ap.add_argument("--shape", default="recompute", choices=["recompute", "prefill", "query"])
+    ap.add_argument("--iters", type=int, default=20)
+    args = ap.parse_args(argv)
+    name, n_docs, doc_len, n_sys, n_query = WORKLOADS[args.workload]
+    cfg = preset(name)
+    torch.manual_seed(0)
+    if args.kernel == "assemble":
+        bench_assemble(cfg, n_docs, doc_len, n_sys, n_query, args.iters)
+    elif args.kernel == "copy":
+        bench_copy(cfg, n_docs, doc_len, n_sys, n_query, args.iters)
+    else:
+        bench_attention(cfg, n_docs, doc_len, n_sys, n_query, args.iters, args.shape)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
