@@ -22,6 +22,8 @@
 // Few rows (the query forward: tens of rows over a long cache) would leave most CUs idle, so the
 // key range is then split across work groups (split-K): each writes its unnormalised fp32 O and
 // its running (max, sum) to a workspace, and a combine kernel merges the splits per row.
+#include <utility>
+
 #include "common.h"
 #include "../../include/tread_hip.h"
 
@@ -29,9 +31,9 @@ namespace tread {
 
 constexpr int ATT_WAVES = 8;
 constexpr int ATT_THREADS = ATT_WAVES * 64;
-constexpr int ATT_QB = 1;                      // 32-row query blocks per wave
-constexpr int ATT_BM = ATT_WAVES * 32 * ATT_QB;  // rows per work group
+constexpr int ATT_BM = ATT_WAVES * 32;         // rows per work group (32 per wave)
 constexpr int ATT_BK = 64;                     // keys per tile
+constexpr int ATT_NBUF = 3;                    // LDS tile buffers (software pipeline depth)
 constexpr int N_XCD = 8;
 constexpr int ATT_TARGET_WGS = 512;     // split-K when fewer (head, row tile) work groups than this
 constexpr int ATT_MIN_SPLIT_KEYS = 1024;
@@ -102,6 +104,68 @@ __device__ __forceinline__ int wave_min(int v) {
   return v;
 }
 
+// LDS byte address of a pointer into the work group's shared memory (the low 32 bits of its
+// generic address; the LDS aperture is 4 GiB-aligned).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
+
+// V^T fragment halves by inline asm rather than the intrinsic: the compiler would otherwise wait
+// for every outstanding global->LDS load (the next tiles' prefetch) before the first transposing
+// read of a tile. The caller orders the results with lgkm_wait before use.
+template <int OFF>
+__device__ __forceinline__ s16x4_t tr_read(uint32_t addr) {
+  s16x4_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+  return r;
+}
+
+// Wait until at most N LDS operations of this wave are outstanding (they complete in order), and
+// tie the fragments read by tr_read to that point.
+template <int N, int M>
+__device__ __forceinline__ void lgkm_wait(s16x4_t (&v)[M]) {
+  static_assert(M == 4 || M == 8, "fragment count");
+  if constexpr (M == 8)
+    asm volatile("s_waitcnt lgkmcnt(%8)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+                 : "n"(N));
+  else
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : "n"(N));
+}
+
+template <int OFF>
+__device__ __forceinline__ bf16x8_t lds_read128(uint32_t addr) {
+  u32x4_t r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait(bf16x8_t& v) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
+}
+
+template <int... I, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// max over lanes l and l ^ 32 (the two key halves of one query column)
+__device__ __forceinline__ float xhalf_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <int HD>
 __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs a) {
   using SM = AttnSmem<HD>;
@@ -134,27 +198,18 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   const int c = lane & 31, half = lane >> 5;
   const int64_t R = a.n * a.G;
   const int n_shared = a.kseg ? (int)min<int64_t>(a.n_shared, a.t_cap) : 0;
-  // this lane's query column in each of the wave's query blocks
-  bool valid[ATT_QB];
-  int64_t qi[ATT_QB];
-  int qh[ATT_QB], my_end[ATT_QB], my_seg[ATT_QB];
+  // this lane's query column: row r of the head group
+  const int64_t r = (int64_t)tile * ATT_BM + wv * 32 + c;
+  const bool valid = r < R;
+  const int64_t qi = valid ? r / a.G : 0;
+  const int qh = head * a.G + (int)(valid ? r % a.G : 0);
+  int my_end = -1, my_seg = 0;
   int vmax = -1, vmin = 0x7fffffff, smax = 0, smin = 0x7fffffff;
-#pragma unroll
-  for (int b = 0; b < ATT_QB; ++b) {
-    const int64_t r = (int64_t)tile * ATT_BM + (wv * ATT_QB + b) * 32 + c;
-    valid[b] = r < R;
-    qi[b] = valid[b] ? r / a.G : 0;
-    qh[b] = head * a.G + (int)(valid[b] ? r % a.G : 0);
-    my_end[b] = -1;
-    my_seg[b] = 0;
-    if (valid[b]) {
-      my_end[b] = (int)min<int64_t>(max<int64_t>(a.kend[qi[b]], -1), a.t_cap - 1);
-      if (a.kseg) my_seg[b] = (int)min<int64_t>(max<int64_t>(a.kseg[qi[b]], 0), a.t_cap);
-      vmax = max(vmax, my_end[b]);
-      vmin = min(vmin, my_end[b]);
-      smax = max(smax, my_seg[b]);
-      smin = min(smin, my_seg[b]);
-    }
+  if (valid) {
+    my_end = (int)min<int64_t>(max<int64_t>(a.kend[qi], -1), a.t_cap - 1);
+    if (a.kseg) my_seg = (int)min<int64_t>(max<int64_t>(a.kseg[qi], 0), a.t_cap);
+    vmax = vmin = my_end;
+    smax = smin = my_seg;
   }
 
   // ---- work-group key range
@@ -193,26 +248,33 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   const int ntiles = nA + nB;
 
   // ---- Q^T fragments (B operand), resident for the whole kernel
-  bf16x8_t qf[ATT_QB][KS];
-#pragma unroll
-  for (int b = 0; b < ATT_QB; ++b) {
-    const bf16_t* qp = a.q + (qi[b] * a.hq + qh[b]) * HD + half * 8;
+  bf16x8_t qf[KS];
+  {
+    const bf16_t* qp = a.q + (qi * a.hq + qh) * HD + half * 8;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       u32x4_t t = {0, 0, 0, 0};
-      if (valid[b]) t = *reinterpret_cast<const u32x4_t*>(qp + s * 16);
-      qf[b][s] = __builtin_bit_cast(bf16x8_t, t);
+      if (valid) t = *reinterpret_cast<const u32x4_t*>(qp + s * 16);
+      qf[s] = __builtin_bit_cast(bf16x8_t, t);
     }
   }
 
   const bf16_t* kbase = a.k + (int64_t)head * a.t_cap * HD;
   const bf16_t* vbase = a.v + (int64_t)head * a.t_cap * HD;
-  // this lane's part of a V^T fragment read (see lds_read_tr16): tile row (key) offset, and the
-  // column (d) offset within a 32-wide d block
-  const int tr_g = lane >> 4, tr_j = lane & 15;
-  const int tr_row = half * 4 + (tr_j >> 2);
-  const int tr_col = (tr_g & 1) * 16 + (tr_j & 3) * 4;
-  const int tr_swz = SM::v_swz(tr_row);  // equal for every row this lane reads (rows differ by multiples of 8)
+  // this lane's V^T fragment read addresses (see lds_read_tr16) in buffer 0, one per d block:
+  // tile row (key) half * 4 + (lane % 16) / 4, column d * 32 + (lane / 16 % 2) * 16 + lane % 4 * 4
+  uint32_t vaddr[DB];
+  {
+    const int tr_g = lane >> 4, tr_j = lane & 15;
+    const int tr_row = half * 4 + (tr_j >> 2);
+    const int tr_col = (tr_g & 1) * 16 + (tr_j & 3) * 4;
+    const int tr_swz = SM::v_swz(tr_row);  // equal for every row this lane reads (rows differ by multiples of 8)
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const int col = d * 32 + tr_col;
+      vaddr[d] = lds_addr(smem + SM::K_ELEMS + tr_row * HD + (((col >> 3) ^ tr_swz) << 3) + (col & 7));
+    }
+  }
 
   auto tile_bounds = [&](int j, int& s0, int& s1) {
     if (j < nA) {
@@ -223,7 +285,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       s1 = min(s0 + ATT_BK, endB);
     }
   };
-  // Queue the tile's K and V rows straight into LDS buffer `buf`. Load x of this wave fills LDS
+  // Queue tile j's K and V rows straight into LDS buffer `buf`. Load x of this wave fills LDS
   // chunk positions [(x * ATT_WAVES + wv) * 64, +64), lane l position +l; the lane fetches the
   // global chunk that the swizzle places there. Rows past the tile's end re-read its last row
   // (finite data; those keys are masked), so nothing outside the cache is touched.
@@ -236,159 +298,269 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     for (int x = 0; x < K_LD; ++x) {
       const int base = (x * ATT_WAVES + wv) * 64;  // first chunk position of this wave-wide load
       const int pos = base + lane;
-      const int r = pos / KCH, p = pos % KCH;
-      const int64_t grow = min(s0 + r, s1 - 1);
-      lds_load16(kbase + grow * HD + (p ^ SM::k_swz(r)) * 8, Ks + base * 8);
-      lds_load16(vbase + grow * HD + (p ^ SM::v_swz(r)) * 8, Vs + base * 8);
+      const int rr = pos / KCH, p = pos % KCH;
+      const int64_t grow = min(s0 + rr, s1 - 1);
+      lds_load16(kbase + grow * HD + (p ^ SM::k_swz(rr)) * 8, Ks + base * 8);
+      lds_load16(vbase + grow * HD + (p ^ SM::v_swz(rr)) * 8, Vs + base * 8);
     }
   };
 
-  f32x16_t oacc[ATT_QB][DB];
+  f32x16_t oacc[DB];
 #pragma unroll
-  for (int b = 0; b < ATT_QB; ++b)
+  for (int d = 0; d < DB; ++d)
 #pragma unroll
-    for (int d = 0; d < DB; ++d)
-#pragma unroll
-      for (int x = 0; x < 16; ++x) oacc[b][d][x] = 0.f;
-  // running max (log2-scaled units) and sum of this lane's query rows
-  float m_run[ATT_QB], l_run[ATT_QB];
-#pragma unroll
-  for (int b = 0; b < ATT_QB; ++b) {
-    m_run[b] = -1e30f;
-    l_run[b] = 0.f;
-  }
+    for (int x = 0; x < 16; ++x) oacc[d][x] = 0.f;
+  // running max (log2-scaled units, shared by lanes l and l ^ 32) and this lane's partial sums
+  float m_run = -1e30f;
+  float lsum[4] = {0.f, 0.f, 0.f, 0.f};
   const float cs = a.scale_log2;
 
-  if (ntiles > 0) issue_tile(0, 0);
-  for (int j = 0; j < ntiles; ++j) {
-    const int buf = j & 1;
-    // tile j's LDS loads (this wave's) have landed; the barrier makes every wave's visible and
-    // guarantees nobody still reads buffer buf ^ 1 (tile j - 1), which the next loads overwrite
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (j + 1 < ntiles) issue_tile(j + 1, buf ^ 1);
-    const bf16_t* Ks = smem + buf * SM::BUF;
-    const bf16_t* Vs = Ks + SM::K_ELEMS;
+  // this lane's A-operand (K) fragment addresses for the 32-key half 0 of buffer 0, one per
+  // k-step: row c, chunk (2 st + half) swizzled; half 1 and the buffers are fixed offsets
+  uint32_t kaddr[KS];
+#pragma unroll
+  for (int st = 0; st < KS; ++st) kaddr[st] = lds_addr(smem + c * HD + ((2 * st + half) ^ SM::k_swz(c)) * 8);
+  constexpr int NK = 2 * KS;  // K fragments per tile
+  constexpr int RING = 4;     // K fragment reads in flight ahead of the MFMAs
+  constexpr int NV = 2 * DB;  // transposing reads per PV k-step
+
+  // V^T fragments of PV k-step ST from the buffer at byte offset `off`
+  auto v_read = [&](auto st_c, uint32_t off, s16x4_t (&f)[NV]) {
+    constexpr int ST = decltype(st_c)::value;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      f[2 * d] = tr_read<ST * 16 * HD * 2>(vaddr[d] + off);
+      f[2 * d + 1] = tr_read<(ST * 16 + 8) * HD * 2>(vaddr[d] + off);
+    }
+  };
+  // S^T = K Q^T for the tile in buffer `buf`: s[kb] holds keys kb * 32 + (x / 4) * 8 + half * 4 + x % 4
+  // (register x) of this lane's query column. K fragments stream RING reads ahead of the MFMAs;
+  // the first V^T fragments of the tile in buffer `vbuf` (if >= 0) are queued behind the last
+  // K read so that they land while the last QK MFMAs run.
+  auto qk = [&](int buf, f32x16_t (&s)[2], int vbuf, s16x4_t (&v0)[NV]) {
+    const uint32_t ko = (uint32_t)(buf * SM::BUF * 2);
+    const uint32_t vo = (uint32_t)(vbuf * SM::BUF * 2);
+    bf16x8_t kf[NK];
+    static_for<RING>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      kf[i] = lds_read128<(i / KS) * 32 * HD * 2>(kaddr[i % KS] + ko);
+    });
+    static_for<NK>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      constexpr int k_after = (i + RING - 1 < NK - 1 ? i + RING - 1 : NK - 1) - i;
+      if (vbuf >= 0) {
+        if constexpr (i >= NK - RING) lgkm_wait<k_after + NV>(kf[i]);
+        else lgkm_wait<k_after>(kf[i]);
+      } else {
+        lgkm_wait<k_after>(kf[i]);
+      }
+      constexpr int kb = i / KS, st = i % KS;
+      if constexpr (st == 0) {
+        const f32x16_t z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i], qf[st], z, 0, 0, 0);
+      } else {
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i], qf[st], s[kb], 0, 0, 0);
+      }
+      if constexpr (i + RING < NK) {
+        constexpr int m = i + RING;
+        kf[m] = lds_read128<(m / KS) * 32 * HD * 2>(kaddr[m % KS] + ko);
+        if constexpr (m == NK - 1) {
+          if (vbuf >= 0) v_read(std::integral_constant<int, 0>{}, vo, v0);
+        }
+      }
+    });
+  };
+  // visibility mask (tiles crossing a row boundary), row max, lazy rescale of O and the sums:
+  // exponentiate against a stale max m_run and move it only when some row's max outgrew it by
+  // more than 2^8; p then stays <= 256 and the final division by the sum is exact either way
+  auto settle = [&](int j, f32x16_t (&s)[2]) {
     int s0, s1;
     tile_bounds(j, s0, s1);
-
     const bool full = (s1 - s0 == ATT_BK) && (s1 - 1 <= kmin) && (j < nA || s0 >= segmax);
-    // each 32-key half of the tile: S^T = K Q^T for every query block (a K fragment read from
-    // LDS feeds them all), online softmax, then O^T += V^T P^T for those 32 keys
+    if (!full) {
+      asm volatile("");  // keeps this rare path a branch: no speculated predicates on full tiles
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      f32x16_t sacc[ATT_QB];
-#pragma unroll
-      for (int b = 0; b < ATT_QB; ++b)
-#pragma unroll
-        for (int x = 0; x < 16; ++x) sacc[b][x] = 0.f;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const int kr = kb * 32 + c;
-        const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(Ks + kr * HD + ((2 * s + half) ^ SM::k_swz(kr)) * 8);
-#pragma unroll
-        for (int b = 0; b < ATT_QB; ++b)
-          sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[b][s], sacc[b], 0, 0, 0);
-      }
-#pragma unroll
-      for (int b = 0; b < ATT_QB; ++b) {
-        if (!full) {
-#pragma unroll
-          for (int x = 0; x < 16; ++x) {
-            int key = s0 + kb * 32 + (x >> 2) * 8 + half * 4 + (x & 3);
-            bool vis = key < s1 && key <= my_end[b] && (key < n_shared || key >= my_seg[b]);
-            sacc[b][x] = vis ? sacc[b][x] : -INFINITY;
-          }
-        }
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int x = 0; x < 16; ++x) tmax = fmaxf(tmax, sacc[b][x]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        // Lazy rescale: exponentiate against a stale row max m_run and move it (rescaling the
-        // running sum and O) only when some row's max outgrew it by more than 2^8; p then stays
-        // <= 256, and the final division by the sum is exact either way.
-        const float m_cand = fmaxf(m_run[b], tmax * cs);
-        if (__ballot(m_cand > m_run[b] + ATT_RESCALE_LOG2)) {
-          const float corr = __builtin_amdgcn_exp2f(m_run[b] - m_cand);
-          l_run[b] *= corr;
-#pragma unroll
-          for (int d = 0; d < DB; ++d)
-#pragma unroll
-            for (int x = 0; x < 16; ++x) oacc[b][d][x] *= corr;
-          m_run[b] = m_cand;
-        }
-        const float m_use = m_run[b];
-        float rs = 0.f;
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int x = 0; x < 16; ++x) {
-          float p = __builtin_amdgcn_exp2f(fmaf(sacc[b][x], cs, -m_use));
-          sacc[b][x] = p;
-          rs += p;
+          const int key = s0 + kb * 32 + (x >> 2) * 8 + half * 4 + (x & 3);
+          const bool vis = key < s1 && key <= my_end && (key < n_shared || key >= my_seg);
+          s[kb][x] = vis ? s[kb][x] : -INFINITY;
         }
-        rs += __shfl_xor(rs, 32);
-        l_run[b] += rs;
-      }
-      // O^T += V^T P^T over the 2 k-steps (16 keys each) of this half; each V fragment feeds
-      // every query block
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const int s = kb * 2 + h2, base = h2 * 8;
-        bf16x8_t pb[ATT_QB];
-#pragma unroll
-        for (int b = 0; b < ATT_QB; ++b) {
-          u32x4_t pw;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) pw[q] = pack_bf(sacc[b][base + 2 * q], sacc[b][base + 2 * q + 1]);
-          pb[b] = __builtin_bit_cast(bf16x8_t, pw);
-        }
-#pragma unroll
-        for (int d = 0; d < DB; ++d) {
-          // V^T fragment: keys s*16 + half*4 + (0..3) and s*16 + 8 + half*4 + (0..3) of column
-          // d*32 + lane%32, transposed on the fly out of the row-major V tile
-          const int col = d * 32 + tr_col;
-          const bf16_t* vr = Vs + (s * 16 + tr_row) * HD + (((col >> 3) ^ tr_swz) << 3) + (col & 7);
-          const s16x4_t lo = lds_read_tr16(vr);
-          const s16x4_t hi = lds_read_tr16(vr + 8 * HD);
-          const bf16x8_t va = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-          for (int b = 0; b < ATT_QB; ++b)
-            oacc[b][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[b], oacc[b][d], 0, 0, 0);
-        }
-      }
     }
-  }
-
+    float mx[4];
 #pragma unroll
-  for (int b = 0; b < ATT_QB; ++b) {
-    if (!valid[b]) continue;
-    if (a.nsplit > 1) {
-      // partial for the combine kernel: unnormalised O, running max and sum
-      const int64_t p = (((int64_t)split * a.hkv + head) * a.tiles + tile) * ATT_BM + (wv * ATT_QB + b) * 32 + c;
-      float* po = a.ws_o + p * HD;
+    for (int q = 0; q < 4; ++q) {
+      mx[q] = fmaxf(fmaxf(s[0][q], s[0][q + 4]), s[0][q + 8]);
+      mx[q] = fmaxf(fmaxf(mx[q], s[0][q + 12]), s[1][q]);
+      mx[q] = fmaxf(fmaxf(mx[q], s[1][q + 4]), s[1][q + 8]);
+      mx[q] = fmaxf(mx[q], s[1][q + 12]);
+    }
+    const float tmax = xhalf_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])));
+    const float m_cand = fmaxf(m_run, tmax * cs);
+    if (__ballot(m_cand > m_run + ATT_RESCALE_LOG2)) {
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_cand);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) lsum[q] *= corr;
 #pragma unroll
       for (int d = 0; d < DB; ++d)
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          f32x4_t o = {oacc[b][d][g4 * 4 + 0], oacc[b][d][g4 * 4 + 1], oacc[b][d][g4 * 4 + 2], oacc[b][d][g4 * 4 + 3]};
-          *reinterpret_cast<f32x4_t*>(po + d * 32 + g4 * 8 + half * 4) = o;
-        }
-      if (half == 0) {
-        a.ws_ml[p * 2] = m_run[b];
-        a.ws_ml[p * 2 + 1] = l_run[b];
-      }
-      continue;
+        for (int x = 0; x < 16; ++x) oacc[d][x] *= corr;
+      m_run = m_cand;
     }
-    const float inv = l_run[b] > 0.f ? 1.0f / l_run[b] : 0.f;
-    bf16_t* op = a.out + (qi[b] * a.hq + qh[b]) * HD;
+  };
+  // P = exp2(S * scale - m) as the B operand of the 4 PV k-steps (16 keys each); register x of
+  // s[kb] feeds k-step kb * 2 + x / 8
+  auto to_p = [&](f32x16_t (&s)[2], bf16x8_t (&pb)[4]) {
+    const float mu = m_run;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][x], cs, -mu));
+        s[kb][x] = p;
+        lsum[x & 3] += p;
+      }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        u32x4_t pw;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pw[q] = pack_bf(s[kb][h2 * 8 + 2 * q], s[kb][h2 * 8 + 2 * q + 1]);
+        pb[kb * 2 + h2] = __builtin_bit_cast(bf16x8_t, pw);
+      }
+  };
+  // O^T += V^T P^T over the tile in buffer `buf`: k-step st covers tile keys st * 16 + half * 4 +
+  // (0..3) and st * 16 + 8 + half * 4 + (0..3); fragment reads run one k-step ahead of the MFMAs.
+  // v0 holds k-step 0's fragments, already queued.
+  auto pv = [&](int buf, const bf16x8_t (&pb)[4], s16x4_t (&v0)[NV]) {
+    const uint32_t off = (uint32_t)(buf * SM::BUF * 2);
+    s16x4_t v1[NV], v2[NV], v3[NV];
+    auto mm = [&](const s16x4_t (&f)[NV], const bf16x8_t& p) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const bf16x8_t va = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(f[2 * d], f[2 * d + 1], 0, 1, 2, 3, 4, 5, 6, 7));
+        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, p, oacc[d], 0, 0, 0);
+      }
+    };
+    v_read(std::integral_constant<int, 1>{}, off, v1);
+    lgkm_wait<NV>(v0);
+    mm(v0, pb[0]);
+    v_read(std::integral_constant<int, 2>{}, off, v2);
+    lgkm_wait<NV>(v1);
+    mm(v1, pb[1]);
+    v_read(std::integral_constant<int, 3>{}, off, v3);
+    lgkm_wait<NV>(v2);
+    mm(v2, pb[2]);
+    lgkm_wait<0>(v3);
+    mm(v3, pb[3]);
+  };
+
+  // Software pipeline over tiles with ATT_NBUF LDS buffers (tile t in buffer t % ATT_NBUF): one
+  // step computes the scores of tile t + 1 while it exponentiates and accumulates tile t, so the
+  // MFMAs of one product overlap the softmax arithmetic of the other; tile t + ATT_NBUF - 1 is
+  // loaded meanwhile. Each wave's outstanding loads are whole tiles of LPT instructions.
+  constexpr int LPT = 2 * K_LD;
+  if (ntiles > 0) {
+#pragma unroll
+    for (int t = 0; t < ATT_NBUF - 1; ++t)
+      if (t < ntiles) issue_tile(t, t);
+    // tile 0 landed: the tiles queued after it may still fly
+    if constexpr (ATT_NBUF >= 4) {
+      if (ntiles > 2) vm_wait<2 * LPT>();
+      else if (ntiles > 1) vm_wait<LPT>();
+      else vm_wait<0>();
+    } else {
+      if (ntiles > 1) vm_wait<LPT>();
+      else vm_wait<0>();
+    }
+    __syncthreads();
+    // The two waves sharing a SIMD (wave w and w + 4) run the softmax and the MFMA phase of a
+    // step in opposite order, so that after each barrier one of them issues MFMAs while the
+    // other exponentiates: group 0 settles and exponentiates tile j + 1 after its MFMAs, group 1
+    // settles and exponentiates tile j before them.
+    const bool late = wv >= ATT_WAVES / 2;
+    f32x16_t sa[2], sb[2];
+    bf16x8_t pb[4];
+    {
+      s16x4_t unused[NV];
+      qk(0, sa, -1, unused);
+    }
+    int j = 0, bj = 0;  // bj = j % ATT_NBUF
+    if (!late) {
+      settle(0, sa);
+      to_p(sa, pb);
+    }
+    while (j + 1 < ntiles) {
+      // every wave's loads of tile j + 1 landed, and every wave is done with tile j - 1, whose
+      // buffer receives tile j + ATT_NBUF - 1
+      if constexpr (ATT_NBUF >= 4) {
+        if (j + 2 < ntiles) vm_wait<LPT>();
+        else vm_wait<0>();
+      } else {
+        vm_wait<0>();
+      }
+      __syncthreads();
+      const int bn = bj == ATT_NBUF - 1 ? 0 : bj + 1, bprev = bj == 0 ? ATT_NBUF - 1 : bj - 1;
+      if (j + ATT_NBUF - 1 < ntiles) issue_tile(j + ATT_NBUF - 1, bprev);
+      if (late) {
+        settle(j, sa);
+        to_p(sa, pb);
+      }
+      s16x4_t v0[NV];
+      qk(bn, sb, -1, v0);
+      v_read(std::integral_constant<int, 0>{}, (uint32_t)(bj * SM::BUF * 2), v0);
+      pv(bj, pb, v0);
+      ++j;
+      bj = bn;
+      if (!late) {
+        settle(j, sb);
+        to_p(sb, pb);
+      } else {
+        sa[0] = sb[0];
+        sa[1] = sb[1];
+      }
+    }
+    if (late) {
+      settle(j, sa);
+      to_p(sa, pb);
+    }
+    s16x4_t v0[NV];
+    v_read(std::integral_constant<int, 0>{}, (uint32_t)(bj * SM::BUF * 2), v0);
+    pv(bj, pb, v0);
+  }
+
+  if (!valid) return;
+  // row sum over both key halves
+  const float l_run = xhalf_sum((lsum[0] + lsum[1]) + (lsum[2] + lsum[3]));
+  if (a.nsplit > 1) {
+    // partial for the combine kernel: unnormalised O, running max and sum
+    const int64_t p = (((int64_t)split * a.hkv + head) * a.tiles + tile) * ATT_BM + wv * 32 + c;
+    float* po = a.ws_o + p * HD;
 #pragma unroll
     for (int d = 0; d < DB; ++d)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        u32x2_t o = {pack_bf(oacc[b][d][g4 * 4 + 0] * inv, oacc[b][d][g4 * 4 + 1] * inv),
-                     pack_bf(oacc[b][d][g4 * 4 + 2] * inv, oacc[b][d][g4 * 4 + 3] * inv)};
-        *reinterpret_cast<u32x2_t*>(op + d * 32 + g4 * 8 + half * 4) = o;
+        f32x4_t o = {oacc[d][g4 * 4 + 0], oacc[d][g4 * 4 + 1], oacc[d][g4 * 4 + 2], oacc[d][g4 * 4 + 3]};
+        *reinterpret_cast<f32x4_t*>(po + d * 32 + g4 * 8 + half * 4) = o;
       }
+    if (half == 0) {
+      a.ws_ml[p * 2] = m_run;
+      a.ws_ml[p * 2 + 1] = l_run;
+    }
+    return;
   }
+  const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+  bf16_t* op = a.out + (qi * a.hq + qh) * HD;
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      u32x2_t o = {pack_bf(oacc[d][g4 * 4 + 0] * inv, oacc[d][g4 * 4 + 1] * inv),
+                   pack_bf(oacc[d][g4 * 4 + 2] * inv, oacc[d][g4 * 4 + 3] * inv)};
+      *reinterpret_cast<u32x2_t*>(op + d * 32 + g4 * 8 + half * 4) = o;
+    }
 }
 
 // Merge split-K partials: one wave per (kv head, row); each lane owns HD/64 output elements.
@@ -521,7 +693,7 @@ extern "C" int tread_subset_attn_bf16(const void* q, const void* k_cache, const 
     grid = (int64_t)hkv * sp.tiles;
   }
   if (grid > 0x7fffffffLL) return fail(TREAD_ERANGE, "subset_attn: grid too large");
-  size_t smem = (head_dim == 128 ? AttnSmem<128>::BUF : AttnSmem<64>::BUF) * 2 * sizeof(bf16_t);
+  size_t smem = (head_dim == 128 ? AttnSmem<128>::BUF : AttnSmem<64>::BUF) * ATT_NBUF * sizeof(bf16_t);
   hipStream_t s = (hipStream_t)stream;
   if (head_dim == 128)
     hipLaunchKernelGGL(subset_attn_kernel<128>, dim3((unsigned)grid), dim3(ATT_THREADS), smem, s, a);

@@ -21,6 +21,11 @@ CFLAGS = [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
+# per-source extra flags: the attention kernel's online softmax takes maxima of finite or -inf
+# scores only, so NaN-preserving min/max (and the canonicalising moves they need) are dropped
+EXTRA = {"attention": ["-fno-honor-nans"]}
+
+
 def _run(cmd):
     p = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in p.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip())
@@ -36,7 +41,7 @@ def build(verbose=False):
 
     def one(name):
         obj = out / f"{name}.o"
-        return _run([HIPCC, *CFLAGS, "-c", str(HERE / f"{name}.hip"), "-o", str(obj)])
+        return _run([HIPCC, *CFLAGS, *EXTRA.get(name, []), "-c", str(HERE / f"{name}.hip"), "-o", str(obj)])
 
     with ThreadPoolExecutor(jobs) as ex:
         msgs = list(ex.map(one, SOURCES))
