@@ -285,24 +285,34 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       s1 = min(s0 + ATT_BK, endB);
     }
   };
-  // Queue tile j's K and V rows straight into LDS buffer `buf`. Load x of this wave fills LDS
-  // chunk positions [(x * ATT_WAVES + wv) * 64, +64), lane l position +l; the lane fetches the
-  // global chunk that the swizzle places there. Rows past the tile's end re-read its last row
-  // (finite data; those keys are masked), so nothing outside the cache is touched.
+  // Queue tile j's K and V rows straight into LDS buffer `buf`, one wave-wide 16-byte load at a
+  // time (LPT loads per wave and tile). Load x of this wave fills LDS chunk positions
+  // [(x * ATT_WAVES + wv) * 64, +64), lane l position +l; the lane fetches the global chunk that
+  // the swizzle places there. Rows past the tile's end re-read its last row (finite data; those
+  // keys are masked), so nothing outside the cache is touched.
+  constexpr int LPT = 2 * K_LD;
+  int ld_row[K_LD], ld_kch[K_LD], ld_vch[K_LD];
+#pragma unroll
+  for (int x = 0; x < K_LD; ++x) {
+    const int pos = (x * ATT_WAVES + wv) * 64 + lane;
+    ld_row[x] = pos / KCH;
+    ld_kch[x] = ((pos % KCH) ^ SM::k_swz(ld_row[x])) * 8;
+    ld_vch[x] = ((pos % KCH) ^ SM::v_swz(ld_row[x])) * 8;
+  }
+  auto issue_load = [&](int q, int s0, int s1, int buf) {
+    const int x = q >> 1;
+    const int64_t grow = min(s0 + ld_row[x], s1 - 1);
+    bf16_t* dst = smem + buf * SM::BUF + ((q & 1) ? SM::K_ELEMS : 0) + (x * ATT_WAVES + wv) * 64 * 8;
+    if (q & 1)
+      lds_load16(vbase + grow * HD + ld_vch[x], dst);
+    else
+      lds_load16(kbase + grow * HD + ld_kch[x], dst);
+  };
   auto issue_tile = [&](int j, int buf) {
     int s0, s1;
     tile_bounds(j, s0, s1);
-    bf16_t* Ks = smem + buf * SM::BUF;
-    bf16_t* Vs = Ks + SM::K_ELEMS;
 #pragma unroll
-    for (int x = 0; x < K_LD; ++x) {
-      const int base = (x * ATT_WAVES + wv) * 64;  // first chunk position of this wave-wide load
-      const int pos = base + lane;
-      const int rr = pos / KCH, p = pos % KCH;
-      const int64_t grow = min(s0 + rr, s1 - 1);
-      lds_load16(kbase + grow * HD + (p ^ SM::k_swz(rr)) * 8, Ks + base * 8);
-      lds_load16(vbase + grow * HD + (p ^ SM::v_swz(rr)) * 8, Vs + base * 8);
-    }
+    for (int q = 0; q < LPT; ++q) issue_load(q, s0, s1, buf);
   };
 
   f32x16_t oacc[DB];
@@ -334,12 +344,9 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     }
   };
   // S^T = K Q^T for the tile in buffer `buf`: s[kb] holds keys kb * 32 + (x / 4) * 8 + half * 4 + x % 4
-  // (register x) of this lane's query column. K fragments stream RING reads ahead of the MFMAs;
-  // the first V^T fragments of the tile in buffer `vbuf` (if >= 0) are queued behind the last
-  // K read so that they land while the last QK MFMAs run.
-  auto qk = [&](int buf, f32x16_t (&s)[2], int vbuf, s16x4_t (&v0)[NV]) {
+  // (register x) of this lane's query column. K fragments stream RING reads ahead of the MFMAs.
+  auto qk = [&](int buf, f32x16_t (&s)[2]) {
     const uint32_t ko = (uint32_t)(buf * SM::BUF * 2);
-    const uint32_t vo = (uint32_t)(vbuf * SM::BUF * 2);
     bf16x8_t kf[NK];
     static_for<RING>([&](auto I) {
       constexpr int i = decltype(I)::value;
@@ -348,12 +355,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     static_for<NK>([&](auto I) {
       constexpr int i = decltype(I)::value;
       constexpr int k_after = (i + RING - 1 < NK - 1 ? i + RING - 1 : NK - 1) - i;
-      if (vbuf >= 0) {
-        if constexpr (i >= NK - RING) lgkm_wait<k_after + NV>(kf[i]);
-        else lgkm_wait<k_after>(kf[i]);
-      } else {
-        lgkm_wait<k_after>(kf[i]);
-      }
+      lgkm_wait<k_after>(kf[i]);
       constexpr int kb = i / KS, st = i % KS;
       if constexpr (st == 0) {
         const f32x16_t z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -364,9 +366,6 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       if constexpr (i + RING < NK) {
         constexpr int m = i + RING;
         kf[m] = lds_read128<(m / KS) * 32 * HD * 2>(kaddr[m % KS] + ko);
-        if constexpr (m == NK - 1) {
-          if (vbuf >= 0) v_read(std::integral_constant<int, 0>{}, vo, v0);
-        }
       }
     });
   };
@@ -457,11 +456,13 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     mm(v3, pb[3]);
   };
 
-  // Software pipeline over tiles with ATT_NBUF LDS buffers (tile t in buffer t % ATT_NBUF): one
-  // step computes the scores of tile t + 1 while it exponentiates and accumulates tile t, so the
-  // MFMAs of one product overlap the softmax arithmetic of the other; tile t + ATT_NBUF - 1 is
-  // loaded meanwhile. Each wave's outstanding loads are whole tiles of LPT instructions.
-  constexpr int LPT = 2 * K_LD;
+  // Software pipeline over tiles with ATT_NBUF LDS buffers (tile t in buffer t % ATT_NBUF): the
+  // MFMA phase of a step computes the scores of tile t + 1 and accumulates tile t, whose
+  // probabilities the softmax phase produced; tile t + ATT_NBUF - 1 is loaded meanwhile. The two
+  // waves sharing a SIMD (wave w and w + 4) run the softmax and the MFMA phase in opposite order,
+  // so that after each barrier one of them issues MFMAs while the other exponentiates: the early
+  // group settles and exponentiates tile t + 1 after its MFMA phase, the late group tile t before.
+  // Each wave's outstanding global loads are whole tiles of LPT instructions.
   if (ntiles > 0) {
 #pragma unroll
     for (int t = 0; t < ATT_NBUF - 1; ++t)
@@ -476,21 +477,14 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       else vm_wait<0>();
     }
     __syncthreads();
-    // The two waves sharing a SIMD (wave w and w + 4) run the softmax and the MFMA phase of a
-    // step in opposite order, so that after each barrier one of them issues MFMAs while the
-    // other exponentiates: group 0 settles and exponentiates tile j + 1 after its MFMAs, group 1
-    // settles and exponentiates tile j before them.
     const bool late = wv >= ATT_WAVES / 2;
-    f32x16_t sa[2], sb[2];
+    f32x16_t sc[2];
     bf16x8_t pb[4];
-    {
-      s16x4_t unused[NV];
-      qk(0, sa, -1, unused);
-    }
+    qk(0, sc);
     int j = 0, bj = 0;  // bj = j % ATT_NBUF
     if (!late) {
-      settle(0, sa);
-      to_p(sa, pb);
+      settle(0, sc);
+      to_p(sc, pb);
     }
     while (j + 1 < ntiles) {
       // every wave's loads of tile j + 1 landed, and every wave is done with tile j - 1, whose
@@ -503,28 +497,27 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       }
       __syncthreads();
       const int bn = bj == ATT_NBUF - 1 ? 0 : bj + 1, bprev = bj == 0 ? ATT_NBUF - 1 : bj - 1;
-      if (j + ATT_NBUF - 1 < ntiles) issue_tile(j + ATT_NBUF - 1, bprev);
+      const int tl = j + ATT_NBUF - 1;
+      if (tl < ntiles) issue_tile(tl, bprev);
       if (late) {
-        settle(j, sa);
-        to_p(sa, pb);
+        settle(j, sc);
+        to_p(sc, pb);
       }
+      // the scores of tile j are in pb now, so sc takes tile j + 1's
+      qk(bn, sc);
       s16x4_t v0[NV];
-      qk(bn, sb, -1, v0);
       v_read(std::integral_constant<int, 0>{}, (uint32_t)(bj * SM::BUF * 2), v0);
       pv(bj, pb, v0);
       ++j;
       bj = bn;
       if (!late) {
-        settle(j, sb);
-        to_p(sb, pb);
-      } else {
-        sa[0] = sb[0];
-        sa[1] = sb[1];
+        settle(j, sc);
+        to_p(sc, pb);
       }
     }
     if (late) {
-      settle(j, sa);
-      to_p(sa, pb);
+      settle(j, sc);
+      to_p(sc, pb);
     }
     s16x4_t v0[NV];
     v_read(std::integral_constant<int, 0>{}, (uint32_t)(bj * SM::BUF * 2), v0);
