@@ -216,7 +216,11 @@ def layer1_deviation(m, ctx_ids, K, V, all_c, inplace=False):
 
 
 def blend(m, ctx_ids, K, V, candidates, ratio, policy, gen=None, inplace=False, trace=None):
-    """tread/blend.py:133-179. `trace` (a dict, optional) receives dev, top and S for the checks."""
+    """tread/blend.py:133-179. `trace` (a dict, optional) receives dev, top and S for the checks.
+
+    Test hook (not reference behaviour): trace["force_S"], a tensor of candidate positions, replaces
+    the deviation top-k selection, so that a test can compare numerics under one shared selection
+    when two implementations split a near-tie differently."""
     K, V = list(K), list(V)
     if not candidates:
         return K, V, torch.empty(0, dtype=torch.long), 0.0
@@ -233,6 +237,9 @@ def blend(m, ctx_ids, K, V, candidates, ratio, policy, gen=None, inplace=False, 
     elif policy == "deviation":
         dev, h, K[0], V[0], kv1 = layer1_deviation(m, ctx_ids, K, V, all_c, inplace=inplace)
         top = dev.topk(budget).indices
+        if trace is not None and trace.get("force_S") is not None:
+            where = {int(p): i for i, p in enumerate(all_c.tolist())}
+            top = torch.tensor([where[int(p)] for p in trace["force_S"].tolist()], dtype=torch.long)
         if trace is not None:
             trace.update(dev=dev, top=top, all_c=all_c, kv1=kv1)
         S, h, start = all_c[top], h[:, top], 1

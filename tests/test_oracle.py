@@ -375,6 +375,24 @@ def test_deviation_blend_selection_and_eff(om):
     assert all(pos[p] == thr for p in got ^ want)
 
 
+def test_forced_selection_hook(om):
+    """The test hook that hands the oracle a selection: its own selection reproduces the natural
+    run exactly; another one is used as given (sorted) with the same budget."""
+    cfg, m = om
+    prefix, docs, query = _req(cfg)
+    eng = R.Engine(m, R.BlockStore(1 << 30))
+    eng.prefill(prefix, docs, query)
+    t0 = {}
+    a, _, _ = eng.prefill(prefix, docs[::-1], query, ratio=0.25, trace=t0)
+    t1 = {"force_S": t0["S"].flip(0)}
+    b, _, _ = eng.prefill(prefix, docs[::-1], query, ratio=0.25, trace=t1)
+    assert torch.equal(a, b) and torch.equal(t1["S"], t0["S"])
+    other = t0["all_c"][torch.randperm(len(t0["all_c"]), generator=torch.Generator().manual_seed(3))[:len(t0["S"])]]
+    t2 = {"force_S": other}
+    c, _, _ = eng.prefill(prefix, docs[::-1], query, ratio=0.25, trace=t2)
+    assert torch.equal(t2["S"], other.sort().values) and not torch.equal(a, c)
+
+
 def test_blend_with_no_docs_and_zero_budget(om):
     cfg, m = om
     K = [torch.zeros(1, 2, 5, 16)] * cfg.num_hidden_layers
