@@ -200,9 +200,12 @@ class Engine:
         self._sync()
         t2 = time.perf_counter()
 
-        R = make_rows(self.P, torch.arange(T, T + Nq, device=dev))
-        h, d = run_layers(self.P, embed(self.P, query_ids), None, R, Kl, Vl, range(self.P.L), hook=asm.ensure)
-        logits = final_logits(self.P, h, d)
+        if graph is not None and Nq > 0:
+            logits = self.runner.query(graph, query_ids, T, hook=asm.ensure)
+        else:
+            R = make_rows(self.P, torch.arange(T, T + Nq, device=dev))
+            h, d = run_layers(self.P, embed(self.P, query_ids), None, R, Kl, Vl, range(self.P.L), hook=asm.ensure)
+            logits = final_logits(self.P, h, d)
         self._sync()
         t3 = time.perf_counter()
         st.t = dict(assemble=t1 - t0, blend=t2 - t1, query=t3 - t2, ttft=t3 - t0)

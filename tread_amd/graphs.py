@@ -14,8 +14,10 @@ it and stays valid until the next request replays the same bucket.
 from collections import OrderedDict
 
 import torch
+import torch.nn.functional as F
 
-from tread_amd.forward import alloc_cache, make_rows, run_layers
+from tread_amd import _hip
+from tread_amd.forward import alloc_cache, embed, make_rows, run_layers
 
 
 def _bucket(n, T, n_min=64, n_step=256, t_step=1024):
@@ -33,8 +35,52 @@ def _q_room(n_query):
     return 256 * max(1, -(-n_query // 256))
 
 
+def _q_bucket(n_query):
+    """Query rows of a captured query forward: a power of two >= 8 up to 256, then multiples of 256."""
+    if n_query <= 256:
+        return max(8, 1 << (n_query - 1).bit_length())
+    return -(-n_query // 256) * 256
+
+
+def _capture(body, device):
+    """Warm `body` up twice on a side stream (default priority), then capture it."""
+    s = torch.cuda.Stream(device=device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            body()
+    torch.cuda.current_stream(device).wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = body()
+    return graph, out
+
+
+class _QueryGraph:
+    """The query forward (all layers, then the final norm and lm_head on the last real row) over
+    a bucket's cache for nq padded query rows at positions T, T+1, ...; padded rows sit after the
+    real ones, in the bucket's spare rows, and no real row can see them."""
+
+    def __init__(self, P, g, nq, device):
+        self.nq = nq
+        self.ids = torch.zeros(nq, dtype=torch.int64, device=device)
+        # capture-time positions: the top rows of the bucket, never part of an assembled context
+        self.pos = torch.arange(g.t_cap - nq, g.t_cap, dtype=torch.int64, device=device)
+        self.last = torch.zeros(1, dtype=torch.int64, device=device)
+
+        def body():
+            R = make_rows(P, self.pos)
+            h, d = run_layers(P, embed(P, self.ids), None, R, g.Kl, g.Vl, range(P.L))
+            _, x = _hip.add_rmsnorm(h.index_select(0, self.last), P.norm, P.eps, delta=d.index_select(0, self.last))
+            return F.linear(x, P.lm_head)[0]
+
+        self.graph, self.out = _capture(body, device)
+
+
 class _Graph:
     def __init__(self, P, start, nb, Tb, t_cap, device, trim_last):
+        self.t_cap = t_cap
+        self.queries = {}  # nq -> _QueryGraph over this bucket's cache
         self.K, self.V = alloc_cache(P, t_cap, device)
         self.K.zero_()
         self.V.zero_()
@@ -47,15 +93,7 @@ class _Graph:
             R = make_rows(P, self.S)
             return run_layers(P, self.h, None, R, self.Kl, self.Vl, range(start, P.L), kv_only_last=trim_last)
 
-        s = torch.cuda.Stream(device=device)  # default priority
-        s.wait_stream(torch.cuda.current_stream(device))
-        with torch.cuda.stream(s):
-            for _ in range(2):
-                body()
-        torch.cuda.current_stream(device).wait_stream(s)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.out = body()
+        self.graph, self.out = _capture(body, device)
 
 
 class SubsetRunner:
@@ -91,8 +129,33 @@ class SubsetRunner:
     @torch.inference_mode()
     def cache_for(self, start, n, T, n_query, device):
         """The bucket graph serving a request that recomputes n rows from layer `start` over a
-        T-row context followed by n_query query rows; its .K/.V are the cache to assemble into."""
-        return self._graph(start, n, T, n_query, device)
+        T-row context followed by n_query query rows; its .K/.V are the cache to assemble into.
+        The query forward for n_query rows is captured with it (before anything is assembled)."""
+        g = self._graph(start, n, T, n_query, device)
+        nq = _q_bucket(n_query)
+        if n_query > 0 and nq not in g.queries:
+            g.queries[nq] = _QueryGraph(self.P, g, nq, device)
+            self.captures += 1
+        return g
+
+    @torch.inference_mode()
+    def query(self, g, ids, T, hook=None):
+        """Replay the captured query forward of bucket `g` for query token ids at rows T.. of its
+        cache; returns the last query row's logits [vocab]. `hook(l)` runs for every layer first."""
+        n = ids.numel()
+        q = g.queries.get(_q_bucket(n))
+        if q is None or T + q.nq > g.t_cap:
+            raise ValueError(f"no captured query forward for {n} rows at T={T} in this bucket")
+        if hook is not None:
+            for l in range(self.P.L):
+                hook(l)
+        q.ids[:n].copy_(ids)
+        if n < q.nq:
+            q.ids[n:].zero_()
+        torch.arange(T, T + q.nq, out=q.pos)
+        q.last.fill_(n - 1)
+        q.graph.replay()
+        return q.out
 
     @torch.inference_mode()
     def run(self, g, h, S, T, hook=None):
