@@ -36,7 +36,7 @@ constexpr int ATT_BK = 64;                     // keys per tile
 constexpr int ATT_NBUF = 3;                    // LDS tile buffers (software pipeline depth)
 constexpr int N_XCD = 8;
 constexpr int ATT_TARGET_WGS = 512;     // split-K when fewer (head, row tile) work groups than this
-constexpr int ATT_MIN_SPLIT_KEYS = 1024;
+constexpr int ATT_MIN_SPLIT_KEYS = 512;
 
 struct AttnArgs {
   const bf16_t* q;
@@ -96,6 +96,16 @@ constexpr float ATT_RESCALE_LOG2 = 8.0f;  // keep a stale row max until it is 2^
 __device__ __forceinline__ int wave_max(int v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
   return v;
 }
 __device__ __forceinline__ int wave_min(int v) {
@@ -556,42 +566,71 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     }
 }
 
-// Merge split-K partials: one wave per (kv head, row); each lane owns HD/64 output elements.
+// Merge split-K partials: one work group per (kv head, row). The split maxima and sums go through
+// LDS; each thread then owns 4 output elements of one split group (every SG-th split), and the
+// groups' weighted partial sums are reduced in LDS.
+constexpr int CMB_THREADS = 256;
+constexpr int CMB_MAX_SPLITS = 1024;
 template <int HD>
-__global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
-  constexpr int EPL = HD / 64;
-  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+__global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(const AttnArgs a) {
+  constexpr int DQ = HD / 4;              // float4 groups of a row
+  constexpr int SG = CMB_THREADS / DQ;    // split groups
+  __shared__ float sm_w[CMB_MAX_SPLITS];  // split weight exp2(m_s - M) (0 for empty splits)
+  __shared__ float red[CMB_THREADS / 64];
+  __shared__ f32x4_t part[SG][DQ];
   const int64_t R = a.n * a.G;
-  if (w >= (int64_t)a.hkv * R) return;
+  const int64_t w = blockIdx.x;
   const int head = (int)(w / R);
   const int64_t r = w % R;
   const int tile = (int)(r / ATT_BM), in_tile = (int)(r % ATT_BM);
-  const int64_t qi = r / a.G;
-  const int qh = head * a.G + (int)(r % a.G);
   const int64_t stride = (int64_t)a.hkv * a.tiles * ATT_BM;
   const int64_t p0 = ((int64_t)head * a.tiles + tile) * ATT_BM + in_tile;
-  float M = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.ws_ml[(p0 + s * stride) * 2]);
-  float L = 0.f, acc[EPL];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  // global max of the split maxima
+  float m = -INFINITY;
+  for (int s = t; s < a.nsplit; s += CMB_THREADS) m = fmaxf(m, a.ws_ml[(p0 + s * stride) * 2]);
+  m = wave_max_f(m);
+  if (lane == 0) red[wv] = m;
+  __syncthreads();
+  float M = red[0];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  for (int s = 0; s < a.nsplit; ++s) {
+  for (int q = 1; q < CMB_THREADS / 64; ++q) M = fmaxf(M, red[q]);
+  __syncthreads();
+  // weights and the weighted sum of the split sums
+  float lw = 0.f;
+  for (int s = t; s < a.nsplit; s += CMB_THREADS) {
     const int64_t p = p0 + s * stride;
     const float l = a.ws_ml[p * 2 + 1];
-    if (l == 0.f) continue;  // empty split
-    const float wgt = __builtin_amdgcn_exp2f(a.ws_ml[p * 2] - M);
-    L += wgt * l;
+    const float wgt = l > 0.f ? __builtin_amdgcn_exp2f(a.ws_ml[p * 2] - M) : 0.f;
+    sm_w[s] = wgt;
+    lw += wgt * l;
+  }
+  lw = wave_sum_f(lw);
+  if (lane == 0) red[wv] = lw;
+  __syncthreads();
+  float L = 0.f;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] += wgt * a.ws_o[p * HD + lane * EPL + e];
+  for (int q = 0; q < CMB_THREADS / 64; ++q) L += red[q];
+  // this thread's 4 elements over its split group
+  const int dq = t % DQ, sg = t / DQ;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = sg; s < a.nsplit; s += SG) {
+    const float wgt = sm_w[s];
+    if (wgt == 0.f) continue;
+    const f32x4_t o = *reinterpret_cast<const f32x4_t*>(a.ws_o + (p0 + s * stride) * HD + dq * 4);
+    acc += wgt * o;
   }
+  part[sg][dq] = acc;
+  __syncthreads();
+  if (sg != 0) return;
+#pragma unroll
+  for (int g = 1; g < SG; ++g) acc += part[g][dq];
   const float inv = L > 0.f ? 1.0f / L : 0.f;
-  bf16_t* op = a.out + (qi * a.hq + qh) * HD + lane * EPL;
-  if constexpr (EPL == 2) {
-    *reinterpret_cast<uint32_t*>(op) = pack_bf(acc[0] * inv, acc[1] * inv);
-  } else {
-    op[0] = f2bf(acc[0] * inv);
-  }
+  const int64_t qi = r / a.G;
+  const int qh = head * a.G + (int)(r % a.G);
+  bf16_t* op = a.out + (qi * a.hq + qh) * HD + dq * 4;
+  const u32x2_t o2 = {pack_bf(acc[0] * inv, acc[1] * inv), pack_bf(acc[2] * inv, acc[3] * inv)};
+  *reinterpret_cast<u32x2_t*>(op) = o2;
 }
 
 struct SplitPlan {
@@ -609,6 +648,7 @@ static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
     int64_t want = (ATT_TARGET_WGS + base - 1) / base;
     int64_t most = t_cap / ATT_MIN_SPLIT_KEYS;
     int64_t ns = want < most ? want : most;
+    if (ns > CMB_MAX_SPLITS) ns = CMB_MAX_SPLITS;
     if (ns > 1) {
       int64_t len = (t_cap + ns - 1) / ns;
       len = (len + ATT_BK - 1) / ATT_BK * ATT_BK;
@@ -694,11 +734,10 @@ extern "C" int tread_subset_attn_bf16(const void* q, const void* k_cache, const 
     hipLaunchKernelGGL(subset_attn_kernel<64>, dim3((unsigned)grid), dim3(ATT_THREADS), smem, s, a);
   int rc = check_launch("subset_attn");
   if (rc || sp.nsplit <= 1) return rc;
-  const int64_t waves = (int64_t)hkv * n * a.G;
-  const int64_t blocks = (waves + 3) / 4;
+  const int64_t blocks = (int64_t)hkv * n * a.G;
   if (head_dim == 128)
-    hipLaunchKernelGGL(attn_combine_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(attn_combine_kernel<128>, dim3((unsigned)blocks), dim3(CMB_THREADS), 0, s, a);
   else
-    hipLaunchKernelGGL(attn_combine_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(attn_combine_kernel<64>, dim3((unsigned)blocks), dim3(CMB_THREADS), 0, s, a);
   return check_launch("subset_attn combine");
 }
