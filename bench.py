@@ -220,6 +220,11 @@ def main():
         wall = (time.perf_counter() - t0) / args.steps
         assert st.hits == 1 + n_docs and st.misses == 0
         log(f"[bench] timed: median ttft {statistics.median(ttfts) * 1e3:.1f} ms, wall/step {wall * 1e3:.1f} ms")
+        if eng.last_selected is not None:
+            S = eng.last_selected.double()
+            flop = 4 * cfg.num_attention_heads * cfg.head_dim * float((S + 1).sum())
+            log(f"[bench] recompute: {S.numel()} rows, mean position {float(S.mean()):.0f}, "
+                f"attention {flop:.3e} FLOP per layer")
         full_ms = None
         if args.full_reps > 0:
             prefill_full(model, system, order, query)
