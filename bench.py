@@ -28,6 +28,9 @@ HBM_PEAK_GBS = 8000.0
 # WRITE_SIZE x 1.0: the factors a plain copy of known size reads on MI355X); the profiler cannot
 # run inside this process, so the figure is carried here for the workload it was measured on.
 MEASURED_ASSEMBLE_TRAFFIC = {"qwen2.5-7b-32k": 3677613000}
+# doc blocks the GPU tier holds (with the prefix block); the rest spill to the pinned-host tier
+# and are copied back per request on the store's copy streams (None: everything stays on the GPU)
+GPU_TIER_DOCS = {"qwen2.5-1.5b-16k": 8}
 WORKLOADS = {
     # name: (preset, n_docs, doc_len, n_system, n_query)
     "qwen2.5-7b-32k": ("qwen2.5-7b", 32, 1000, 64, 32),
@@ -59,13 +62,19 @@ def time_assemble(eng, system, docs, order, n_query, iters=20):
     from tread_amd.forward import alloc_cache
     from tread_amd.store import block_key
     P = eng.P
+    dev = system.device
+
+    def on_gpu(key):  # blocks of either tier; host-tier ones are copied up for this measurement
+        b = eng.store.blocks.get(key) or eng.store.cpu_blocks[key]
+        return b, b.K.to(dev), b.V.to(dev)
+
     pkey = block_key(*eng.sig, "", "prefix", system)
-    pb = eng.store.blocks[pkey]
-    srcs = [(pb.K, pb.V, 0, 0)]
+    pb, pK, pV = on_gpu(pkey)
+    srcs = [(pK, pV, 0, 0)]
     off = pb.n_tokens
     for i in order:
-        b = eng.store.blocks[block_key(*eng.sig, pkey, docs[i])]
-        srcs.append((b.K, b.V, off, off - b.base))
+        b, bK, bV = on_gpu(block_key(*eng.sig, pkey, docs[i]))
+        srcs.append((bK, bV, off, off - b.base))
         off += b.n_tokens
     T = off
     K, V = alloc_cache(P, T + n_query, system.device)
@@ -176,6 +185,8 @@ def main():
     ap.add_argument("--full-reps", type=int, default=3, help="full-prefill reps for the TTFT denominator (0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gpu-tier-docs", type=int, default=None,
+                    help="doc blocks the GPU tier holds (default: the workload's setting; -1: all)")
     ap.add_argument("--no-tune", action="store_true",
                     help="library-default GEMM solutions (default: the measured per-shape table in "
                          "tread_amd/tuning, applied through PyTorch TunableOp)")
@@ -201,7 +212,17 @@ def main():
     model = synthetic_model(cfg, dev, torch.bfloat16, seed=0)
     system, docs, query, perm = make_inputs(cfg, n_docs, doc_len, n_sys, n_query, dev)
     T = n_sys + n_docs * doc_len
-    eng = Engine(model, BlockStore(1 << 40), graphs=not args.eager)
+    tier_docs = GPU_TIER_DOCS.get(args.workload) if args.gpu_tier_docs is None else args.gpu_tier_docs
+    if tier_docs is not None and tier_docs < 0:
+        tier_docs = None
+    budget = 1 << 40
+    if tier_docs is not None:
+        per_token = 2 * cfg.num_hidden_layers * cfg.num_key_value_heads * cfg.head_dim * 2
+        budget = per_token * (n_sys + tier_docs * doc_len)
+        log(f"[bench] GPU tier: prefix + {tier_docs} of {n_docs} doc blocks ({budget / 1e6:.0f} MB); "
+            "the rest live in pinned host memory")
+    store = BlockStore(budget, 1 << 40)
+    eng = Engine(model, store, graphs=not args.eager)
     with torch.inference_mode():
         log("[bench] pass 1: cold prefill of every doc (packed block-diagonal)")
         _, _, st1 = eng.prefill(system, docs, query)
@@ -211,6 +232,7 @@ def main():
             log(f"[bench] warmup {i}: ttft {st.t['ttft'] * 1e3:.1f} ms hits {st.hits} misses {st.misses}")
         torch.cuda.synchronize()
         ttfts, stages = [], []
+        c0 = store.stats.cpu_hits
         t0 = time.perf_counter()
         for i in range(args.steps):
             _, _, st = eng.prefill(system, order, query, ratio=args.ratio)
@@ -219,6 +241,11 @@ def main():
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) / args.steps
         assert st.hits == 1 + n_docs and st.misses == 0
+        host_hits = (store.stats.cpu_hits - c0) / args.steps
+        if host_hits:
+            per_token = 2 * cfg.num_hidden_layers * cfg.num_key_value_heads * cfg.head_dim * 2
+            log(f"[bench] host-tier hits per request: {host_hits:.1f} blocks "
+                f"(~{host_hits * doc_len * per_token / 1e6:.0f} MB H2D, as many evicted D2H)")
         log(f"[bench] timed: median ttft {statistics.median(ttfts) * 1e3:.1f} ms, wall/step {wall * 1e3:.1f} ms")
         if eng.last_selected is not None:
             S = eng.last_selected.double()
@@ -257,7 +284,8 @@ def main():
         "config": {"workload": args.workload, "model": preset_name, "context_tokens": T, "docs": n_docs,
                    "doc_len": doc_len, "system": n_sys, "query": n_query, "recompute_ratio": args.ratio,
                    "policy": "deviation", "hipgraph": not args.eager, "gemm_tuning": not args.no_tune,
-                   "parallelism": "single GPU"},
+                   "gpu_tier_docs": n_docs if tier_docs is None else tier_docs,
+                   "host_tier_hits_per_request": host_hits, "parallelism": "single GPU"},
         "stages_ms": med,
         "ttft_full_prefill_ms": None if full_ms is None else round(full_ms, 2),
         "speedup_vs_full_prefill": None if full_ms is None else round(full_ms / ttft_ms, 2),

@@ -130,6 +130,14 @@ int tread_silu_mul_bf16(const void* gate_up, int64_t n, int inter, void* out, tr
  */
 int tread_copy_async(void* dst, const void* src, size_t bytes, tread_stream_t stream, tread_event_t done);
 
+/* Layer-major schedule of such copies: for l in [0, n_layers): the per_layer copies
+ * dst[l * per_layer + i] <- src[l * per_layer + i] (bytes[...]) in order, then layer_done[l]
+ * recorded (NULL array or entries skip it). One call queues the slices of every block a request
+ * promotes from the host tier, layer 0 of all blocks first. Replaces the per-block
+ * b.K.to(device, non_blocking=True) of tread/store.py:75-76. */
+int tread_copy_layers_async(void* const* dst, const void* const* src, const size_t* bytes, int per_layer,
+                            int n_layers, tread_stream_t stream, const tread_event_t* layer_done);
+
 #ifdef __cplusplus
 }
 #endif

@@ -135,3 +135,15 @@ def test_prepare_fuses_a_transformers_model():
     assert torch.equal(P.layers[0].wqkv, torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight]))
     assert torch.equal(P.inv_freq, hf.model.rotary_emb.inv_freq.float())
     assert P.hd == 8 and P.hq == 4 and P.hkv == 2
+
+
+@pytest.mark.parametrize("L", [1, 2, 3, 24, 28, 80])
+def test_tier_move_layer_groups_tile_the_layers(L):
+    """Host-tier promotions move layers in groups that cover [0, L) in order, small ones first."""
+    from tread_amd import _hip as H
+    g = H.layer_groups(L)
+    assert g[0][0] == 0 and g[-1][1] == L
+    assert all(a < b for a, b in g) and all(g[i][1] == g[i + 1][0] for i in range(len(g) - 1))
+    widths = [b - a for a, b in g]
+    assert all(widths[i] <= widths[i + 1] for i in range(len(widths) - 2))  # the last may be cut short
+    assert widths[0] <= 2

@@ -10,7 +10,7 @@ from pathlib import Path
 import torch  # loads torch's HIP runtime first, so the library below binds to the same one
 
 LIB_PATH = Path(__file__).resolve().with_name("libtread_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 c_i64, c_int, c_void, c_float, c_size = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
 P_I64 = ctypes.POINTER(ctypes.c_int64)
@@ -40,6 +40,7 @@ _SIGS = {
     "tread_add_rmsnorm_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_int, c_void, c_void, c_void]),
     "tread_silu_mul_bf16": (c_int, [c_void, c_i64, c_int, c_void, c_void]),
     "tread_copy_async": (c_int, [c_void, c_void, c_size, c_void, c_void]),
+    "tread_copy_layers_async": (c_int, [c_void, c_void, c_void, c_int, c_int, c_void, c_void]),
 }
 
 _lib = None
@@ -253,6 +254,49 @@ def subset_attn(q, k_cache, v_cache, kend, hq, hkv, hd, scale, kseg=None, n_shar
 
 
 # ------------------------------------------------------------------------------------------- (d)
+
+def layer_groups(L):
+    """Layer groups of a tier move, small first (the first layers are needed first): 2, 2, 4, 4, 8,
+    8, ... layers."""
+    groups, a, size = [], 0, 2
+    while a < L:
+        for _ in range(2):
+            if a < L:
+                groups.append((a, min(L, a + size)))
+                a = min(L, a + size)
+        size *= 2
+    return groups
+
+
+def copy_layers(dsts, srcs, stream, groups, events):
+    """Layer-major DMAs for blocks stacked by layer: dsts, srcs are equal-length lists of
+    contiguous [L, ...] tensors (pinned host <-> device). For each layer group (a, b) in order, the
+    slices [a, b) of every pair are queued on `stream` (one DMA per tensor), then that group's
+    torch.cuda.Event is recorded. One library call."""
+    import numpy as np
+    n, G = len(dsts), len(groups)
+    if n == 0 or G == 0:
+        return
+    db = np.empty(n, dtype=np.uint64)
+    sb = np.empty(n, dtype=np.uint64)
+    lb = np.empty(n, dtype=np.uint64)
+    for i, (d, s_) in enumerate(zip(dsts, srcs)):
+        if d.shape != s_.shape or d.dtype != s_.dtype or d.shape[0] < groups[-1][1]:
+            raise ValueError(f"copy_layers: pair {i} shapes {tuple(d.shape)} / {tuple(s_.shape)}")
+        if not (d.is_contiguous() and s_.is_contiguous()):
+            raise ValueError(f"copy_layers: pair {i} must be contiguous")
+        db[i], sb[i], lb[i] = d.data_ptr(), s_.data_ptr(), d[0].numel() * d.element_size()
+    first = np.array([g[0] for g in groups], dtype=np.uint64)[:, None]
+    width = np.array([g[1] - g[0] for g in groups], dtype=np.uint64)[:, None]
+    dst = np.ascontiguousarray(db[None, :] + first * lb[None, :])
+    src = np.ascontiguousarray(sb[None, :] + first * lb[None, :])
+    size = np.ascontiguousarray(width * lb[None, :])
+    for e in events:
+        e.record(stream)  # creates the event; the library records it again after its group
+    ev = np.array([e.cuda_event for e in events], dtype=np.uint64)
+    _check("tread_copy_layers_async", lib().tread_copy_layers_async(
+        dst.ctypes.data, src.ctypes.data, size.ctypes.data, n, G, ctypes.c_void_p(stream.cuda_stream), ev.ctypes.data))
+
 
 def copy_async(dst, src, stream, event=None):
     """DMA src -> dst (pinned host <-> device) on `stream` (a torch.cuda.Stream); records `event`."""

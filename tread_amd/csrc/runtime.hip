@@ -34,7 +34,27 @@ int check_launch(const char* what) {
 
 extern "C" const char* tread_last_error(void) { return tread::g_err; }
 
-extern "C" int tread_abi_version(void) { return 2; }
+extern "C" int tread_abi_version(void) { return 3; }
+
+extern "C" int tread_copy_layers_async(void* const* dst, const void* const* src, const size_t* bytes, int per_layer,
+                                       int n_layers, tread_stream_t stream, const tread_event_t* layer_done) {
+  if (per_layer < 0 || n_layers < 0 || (per_layer > 0 && n_layers > 0 && (!dst || !src || !bytes)))
+    return tread::fail(TREAD_EINVAL, "tread_copy_layers_async: bad arguments");
+  for (int l = 0; l < n_layers; ++l) {
+    for (int i = 0; i < per_layer; ++i) {
+      const int64_t k = (int64_t)l * per_layer + i;
+      if (bytes[k] == 0) continue;
+      if (!dst[k] || !src[k]) return tread::fail(TREAD_EINVAL, "tread_copy_layers_async: null pointer at %lld", (long long)k);
+      hipError_t e = hipMemcpyAsync(dst[k], src[k], bytes[k], hipMemcpyDefault, (hipStream_t)stream);
+      if (e != hipSuccess) return tread::fail((int)e, "tread_copy_layers_async: copy %lld: %s", (long long)k, hipGetErrorString(e));
+    }
+    if (layer_done && layer_done[l]) {
+      hipError_t e = hipEventRecord((hipEvent_t)layer_done[l], (hipStream_t)stream);
+      if (e != hipSuccess) return tread::fail((int)e, "tread_copy_layers_async: event record: %s", hipGetErrorString(e));
+    }
+  }
+  return 0;
+}
 
 extern "C" int tread_copy_async(void* dst, const void* src, size_t bytes, tread_stream_t stream,
                                 tread_event_t done) {

@@ -137,6 +137,7 @@ class Engine:
         if not miss:
             return blocks
         st.misses += len(miss)
+        self.store.flush()  # the packed prefill reads the prefix block
         P = pb.n_tokens
         ids = torch.cat([docs[i] for i in miss])
         n, dev = len(ids), ids.device
@@ -164,8 +165,9 @@ class Engine:
         self._sync()
         t0 = time.perf_counter()
 
-        pkey, pb = self.prefix_block(prefix_ids, st, namespace)
-        blocks = self.doc_blocks(pkey, pb, docs, st)
+        with self.store.batch():  # host-tier hits share one layer-major H2D schedule
+            pkey, pb = self.prefix_block(prefix_ids, st, namespace)
+            blocks = self.doc_blocks(pkey, pb, docs, st)
         Pn = pb.n_tokens
         T = Pn + sum(len(d) for d in docs)
         Nq = len(query_ids)

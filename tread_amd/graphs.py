@@ -9,7 +9,9 @@ and their hidden rows copied in (a few MB). Padding follows the reference: padde
 sit at positions T, T+1, ... inside the bucket's spare rows, which no real query can see.
 
 Each bucket holds one [L, 1, kv, t_cap, hd] K/V pair; the cache returned by the engine aliases
-it and stays valid until the next request replays the same bucket.
+it and stays valid until the next request replays the same bucket. The loop is captured as one
+graph per layer (chained through static hidden-state tensors), so a replay waits for a layer's
+host-tier copies only right before that layer: the block-tier DMAs overlap the recompute.
 """
 from collections import OrderedDict
 
@@ -42,7 +44,7 @@ def _q_bucket(n_query):
     return -(-n_query // 256) * 256
 
 
-def _capture(body, device):
+def _capture(body, device, pool=None):
     """Warm `body` up twice on a side stream (default priority), then capture it."""
     s = torch.cuda.Stream(device=device)
     s.wait_stream(torch.cuda.current_stream(device))
@@ -51,7 +53,7 @@ def _capture(body, device):
             body()
     torch.cuda.current_stream(device).wait_stream(s)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, pool=pool):
         out = body()
     return graph, out
 
@@ -78,7 +80,11 @@ class _QueryGraph:
 
 
 class _Graph:
-    def __init__(self, P, start, nb, Tb, t_cap, device, trim_last):
+    """The recompute loop of one bucket, captured as one graph per group of `seg` layers that
+    chain through static hidden-state tensors: a replay can then wait for each layer's host-tier
+    copies (and assemble them) right before that layer, instead of before the whole loop."""
+
+    def __init__(self, P, start, nb, Tb, t_cap, device, trim_last, seg=1):
         self.t_cap = t_cap
         self.queries = {}  # nq -> _QueryGraph over this bucket's cache
         self.K, self.V = alloc_cache(P, t_cap, device)
@@ -88,25 +94,43 @@ class _Graph:
         self.h = torch.zeros(nb, P.H, dtype=P.embed.dtype, device=device)
         self.S = torch.arange(nb, dtype=torch.int64, device=device)
         self.nb, self.Tb, self.start = nb, Tb, start
+        self.pool = torch.cuda.graph_pool_handle()
+        layers = list(range(start, P.L))
+        groups = [layers[i:i + seg] for i in range(0, len(layers), seg)]
+        self.segs = []
+        carry = {}
 
-        def body():
-            R = make_rows(P, self.S)
-            return run_layers(P, self.h, None, R, self.Kl, self.Vl, range(start, P.L), kv_only_last=trim_last)
+        for gi, ls in enumerate(groups):
+            last = gi == len(groups) - 1
 
-        self.graph, self.out = _capture(body, device)
+            def body(ls=ls, gi=gi, last=last):
+                if gi == 0:
+                    carry["R"] = make_rows(P, self.S)
+                    h, delta = self.h, None
+                else:
+                    h, delta = carry["out"][gi - 1]
+                return run_layers(P, h, delta, carry["R"], self.Kl, self.Vl, ls, kv_only_last=trim_last and last)
+
+            carry.setdefault("out", [])
+            graph, out = _capture(body, device, self.pool)
+            carry["out"].append(out)
+            self.segs.append((ls, graph))
+        self._carry = carry  # keeps the chained static tensors alive
+        self.out = carry["out"][-1]
 
 
 class SubsetRunner:
     """One captured graph per (start layer, rows bucket, cache bucket, query room); LRU of
     `max_graphs`. `max_ctx`: contexts above it run eagerly (None: always graph)."""
 
-    def __init__(self, model, max_graphs=4, max_ctx=None, trim_last=True):
+    def __init__(self, model, max_graphs=4, max_ctx=None, trim_last=True, seg=1):
         from tread_amd.blend import prepared
         self.model = model
         self.P = prepared(model)
         self.max_graphs = max_graphs
         self.max_ctx = max_ctx
         self.trim_last = trim_last
+        self.seg = seg
         self.graphs: "OrderedDict[tuple, _Graph]" = OrderedDict()
         self.captures = 0
 
@@ -120,7 +144,7 @@ class SubsetRunner:
         if g is None:
             while len(self.graphs) >= self.max_graphs:
                 self.graphs.popitem(last=False)
-            g = _Graph(self.P, start, nb, Tb, Tb + key[3], device, self.trim_last)
+            g = _Graph(self.P, start, nb, Tb, Tb + key[3], device, self.trim_last, self.seg)
             self.graphs[key] = g
             self.captures += 1
         self.graphs.move_to_end(key)
@@ -160,18 +184,19 @@ class SubsetRunner:
     @torch.inference_mode()
     def run(self, g, h, S, T, hook=None):
         """Replay layers start..L-1 of bucket graph `g` for sorted positions S (len n <= g.nb) with
-        hidden rows h [n, H] over a T-row context. `hook(l)` runs for every layer first (lazy
-        assembly must complete before the replay reads the cache)."""
+        hidden rows h [n, H] over a T-row context. `hook(l)` runs before the graph segment holding
+        layer l (lazy assembly must complete before the replay reads that layer of the cache)."""
         n = len(S)
         if n > g.nb or T + g.nb - n > g.Tb:
             raise ValueError(f"request (n={n}, T={T}) does not fit bucket (nb={g.nb}, Tb={g.Tb})")
-        if hook is not None:
-            for l in range(g.start, self.P.L):
-                hook(l)
         g.S[:n].copy_(S)
         g.h[:n].copy_(h)
         if n < g.nb:
             g.S[n:].copy_(torch.arange(T, T + g.nb - n, device=S.device))
             g.h[n:].zero_()
-        g.graph.replay()
+        for ls, graph in g.segs:
+            if hook is not None:
+                for l in ls:
+                    hook(l)
+            graph.replay()
         return g.out

@@ -3,18 +3,27 @@
 Same API, keys, LRU order and statistics as tread/store.py:1-125. A block is the K/V of one chunk
 for all layers, stacked [layers, 1, kv_heads, tokens, head_dim], plus the position it was computed
 at (`base`). What differs is how bytes move between tiers:
-  - a host-tier hit (store.py:73-77) allocates the GPU tensors and queues one DMA per layer slice
-    (K then V) from pinned memory on the store's copy stream, recording one event per layer in
-    `Block.ready`; consumers wait on those events (`Block.wait`) on their own stream, so the
-    copy overlaps whatever runs before layer l is needed;
-  - an eviction (store.py:99-115) queues a D2H DMA into freshly allocated pinned memory on the
-    same copy stream after the producing stream's work, instead of a synchronous copy + re-pin.
-    The evicted GPU tensors are kept alive for the copy by the caching allocator's stream record.
-Copies on one stream run in FIFO order, so a later H2D of a block never overtakes its D2H.
+  - a host-tier hit (store.py:73-77) allocates the GPU tensors and queues DMAs from pinned memory
+    on the store's H2D stream in layer groups of growing size (2, 2, 4, 4, 8, 8 layers), one DMA
+    per tensor and group, recording one event per group in `Block.ready` (indexed by layer);
+    consumers wait on those events (`Block.wait`) on their own stream, so the copy of layer l
+    overlaps whatever runs before layer l is needed. Lookups made inside `batch()` share one
+    schedule: group 0 of every promoted block, then group 1, ... so that the first layers of all
+    blocks land first;
+  - an eviction (store.py:99-115) queues a D2H DMA into freshly allocated pinned memory on a
+    second stream, after the producing stream's work (and after the block's own H2D if it was
+    promoted in the same batch), instead of a synchronous copy + re-pin. The evicted GPU tensors
+    are kept alive for the copy by the caching allocator's stream record. A block that came from
+    the host tier keeps its pinned buffers (`shadow`; blocks never change), so evicting it again
+    copies nothing: a working set cycling through a too-small GPU tier moves each block up once
+    per request and never back down.
+A block evicted and promoted again before its D2H was queued forces the pending copies out first,
+so an H2D never reads a host buffer before its D2H filled it.
 The store is single-threaded (callers serialise requests), as in the reference.
 """
 import hashlib
 from collections import OrderedDict
+from contextlib import contextmanager
 from dataclasses import dataclass, field
 from typing import Optional
 
@@ -48,6 +57,8 @@ class Block:
     hits: int = 0
     ready: Optional[list] = field(default=None, repr=False)  # per-layer events of a pending H2D
     host_ready: Optional[object] = field(default=None, repr=False)  # event of a pending D2H
+    # pinned (K, V) a promoted block came from: blocks never change, so evicting it again needs no D2H
+    shadow: Optional[tuple] = field(default=None, repr=False)
 
     @property
     def pending(self):
@@ -70,6 +81,16 @@ class Block:
                 e.synchronize()
 
 
+class _PendingCopy:
+    """host_ready of a host block whose D2H is not queued yet (batched eviction)."""
+
+    def synchronize(self):
+        raise RuntimeError("BlockStore: flush() the batch before reading an evicted block on the host")
+
+
+_Pending = _PendingCopy()
+
+
 @dataclass
 class StoreStats:
     """tread/store.py:44-53."""
@@ -90,63 +111,120 @@ class BlockStore:
         self.blocks: "OrderedDict[str, Block]" = OrderedDict()  # GPU tier
         self.cpu_blocks: "OrderedDict[str, Block]" = OrderedDict()
         self.stats = StoreStats()
-        self._copy_stream = None
+        self._streams = {}  # "h2d" / "d2h" -> torch.cuda.Stream (default priority)
         # (event, tensors) of DMAs in flight: pinned buffers stay referenced until their copy ends,
         # since the DMA is not visible to torch's pinned-memory allocator.
         self._inflight = []
+        self._batch = 0
+        self._h2d = []  # (Block, host K, host V): promotions whose DMAs are not queued yet
+        self._d2h = []  # (GPU Block, host Block): evictions whose DMAs are not queued yet
 
     def _reap(self):
         if self._inflight:
             self._inflight = [(e, refs) for e, refs in self._inflight if not e.query()]
 
     # ---- copy engine
+    def _stream(self, kind, device):
+        s = self._streams.get(kind)
+        if s is None:
+            s = self._streams[kind] = torch.cuda.Stream(device=device)
+        return s
+
     def copy_stream(self, device):
-        if self._copy_stream is None:
-            self._copy_stream = torch.cuda.Stream(device=device)  # default priority
-        return self._copy_stream
+        """The stream host-tier promotions are copied on."""
+        return self._stream("h2d", device)
+
+    @contextmanager
+    def batch(self):
+        """Lookups inside the block share one layer-major H2D schedule, queued on exit (or at an
+        explicit `flush()`, which a caller must make before it reads any block obtained inside)."""
+        self._batch += 1
+        try:
+            yield self
+        finally:
+            self._batch -= 1
+            if self._batch == 0:
+                self.flush()
+
+    def flush(self):
+        """Queue the pending DMAs: promotions layer-major on the H2D stream, then evictions on the
+        D2H stream."""
+        if self._h2d:
+            pend, self._h2d = self._h2d, []
+            dev = pend[0][0].K.device
+            cur = torch.cuda.current_stream(dev)
+            s = self.copy_stream(dev)
+            s.wait_stream(cur)  # the fresh allocations may reuse memory the current stream released
+            for _, hK, hV in pend:  # host buffers filled by a queued D2H (evicted earlier)
+                if getattr(hK, "_tread_ready", None) is not None:
+                    s.wait_event(hK._tread_ready)
+            L = pend[0][0].K.shape[0]
+            groups = _hip.layer_groups(L)
+            gev = [torch.cuda.Event() for _ in groups]
+            _hip.copy_layers([t for b, _, _ in pend for t in (b.K, b.V)], [t for _, hK, hV in pend for t in (hK, hV)],
+                             s, groups, gev)
+            events = [e for (a, b_), e in zip(groups, gev) for _ in range(a, b_)]  # per layer
+            for b, hK, hV in pend:
+                b.K.record_stream(s)
+                b.V.record_stream(s)
+                b.ready = events
+            self._inflight.append((events[-1], tuple(t for _, hK, hV in pend for t in (hK, hV))))
+        if self._d2h:
+            pend, self._d2h = self._d2h, []
+            for gb, hb in pend:
+                self._queue_d2h(gb, hb)
+
+    def _queue_d2h(self, gb, hb):
+        dev = gb.K.device
+        s = self._stream("d2h", dev)
+        s.wait_stream(torch.cuda.current_stream(dev))  # the block's producer lands first
+        if gb.ready is not None:
+            s.wait_event(gb.ready[-1])  # and its own promotion
+        _hip.copy_async(hb.K, gb.K, s)
+        _hip.copy_async(hb.V, gb.V, s)
+        e = torch.cuda.Event()
+        e.record(s)
+        gb.K.record_stream(s)
+        gb.V.record_stream(s)
+        hb.host_ready = e
+        hb.K._tread_ready = e
+        self._inflight.append((e, (hb.K, hb.V)))
 
     def _to_device(self, b: Block):
-        """Queue the H2D of a host-tier block, one DMA pair + event per layer."""
+        """Promote a host-tier block: GPU tensors now, its DMAs with the batch's schedule."""
         dev = b.device
         if not (isinstance(dev, torch.device) and dev.type == "cuda"):
             b.K, b.V = b.K.clone(), b.V.clone()
             return
-        cur = torch.cuda.current_stream(dev)
-        s = self.copy_stream(dev)
-        K = torch.empty(b.K.shape, dtype=b.K.dtype, device=dev)
-        V = torch.empty(b.V.shape, dtype=b.V.dtype, device=dev)
-        s.wait_stream(cur)  # the fresh allocation may reuse memory the current stream just released
-        events = []
-        for l in range(K.shape[0]):
-            _hip.copy_async(K[l], b.K[l], s)
-            _hip.copy_async(V[l], b.V[l], s)
-            e = torch.cuda.Event()
-            e.record(s)
-            events.append(e)
-        K.record_stream(s)
-        V.record_stream(s)
-        self._inflight.append((events[-1], (b.K, b.V)))
-        b.K, b.V, b.ready, b.host_ready = K, V, events, None
+        if b.host_ready is not None and any(hb is b for _, hb in self._d2h):
+            self.flush()  # its D2H is not queued yet: queue it before reading the host buffer
+        hK, hV = b.K, b.V
+        b.K = torch.empty(hK.shape, dtype=hK.dtype, device=dev)
+        b.V = torch.empty(hV.shape, dtype=hV.dtype, device=dev)
+        b.ready, b.host_ready = [], None  # pending: the layer events are set when queued
+        b.shadow = (hK, hV)
+        self._h2d.append((b, hK, hV))
+        if self._batch == 0:
+            self.flush()
 
     def _to_host(self, b: Block) -> Block:
-        """Queue the D2H of an evicted GPU block into new pinned memory; returns the host Block."""
+        """Evict a GPU block into new pinned memory; returns the host Block (its D2H queued with
+        the batch, or now)."""
         if not b.K.is_cuda:
             return Block(K=b.K.clone(), V=b.V.clone(), base=b.base, n_tokens=b.n_tokens, nbytes=b.nbytes,
                          device=b.device, hits=b.hits)
-        dev = b.K.device
-        s = self.copy_stream(dev)
-        s.wait_stream(torch.cuda.current_stream(dev))  # the block's producer and pending H2D land first
+        if b.shadow is not None:  # the pinned copy it was promoted from still holds its data
+            K, V = b.shadow
+            return Block(K=K, V=V, base=b.base, n_tokens=b.n_tokens, nbytes=b.nbytes, device=b.device, hits=b.hits)
         K = torch.empty(b.K.shape, dtype=b.K.dtype, pin_memory=True)
         V = torch.empty(b.V.shape, dtype=b.V.dtype, pin_memory=True)
-        _hip.copy_async(K, b.K, s)
-        _hip.copy_async(V, b.V, s)
-        e = torch.cuda.Event()
-        e.record(s)
-        b.K.record_stream(s)
-        b.V.record_stream(s)
-        self._inflight.append((e, (K, V)))
-        return Block(K=K, V=V, base=b.base, n_tokens=b.n_tokens, nbytes=b.nbytes, device=b.device, hits=b.hits,
-                     host_ready=e)
+        hb = Block(K=K, V=V, base=b.base, n_tokens=b.n_tokens, nbytes=b.nbytes, device=b.device, hits=b.hits,
+                   host_ready=_Pending)
+        if self._batch == 0 and not any(gb is b for gb, _, _ in self._h2d):
+            self._queue_d2h(b, hb)
+        else:
+            self._d2h.append((b, hb))
+        return hb
 
     # ---- tread/store.py API
     def get(self, key):
