@@ -243,9 +243,8 @@ def main():
         assert st.hits == 1 + n_docs and st.misses == 0
         host_hits = (store.stats.cpu_hits - c0) / args.steps
         if host_hits:
-            per_token = 2 * cfg.num_hidden_layers * cfg.num_key_value_heads * cfg.head_dim * 2
-            log(f"[bench] host-tier hits per request: {host_hits:.1f} blocks "
-                f"(~{host_hits * doc_len * per_token / 1e6:.0f} MB H2D; evictions reuse the pinned copies)")
+            log(f"[bench] host-tier hits per request: {host_hits:.1f} of {1 + n_docs} blocks "
+                "(promoted by H2D; evictions reuse the pinned copies)")
         log(f"[bench] timed: median ttft {statistics.median(ttfts) * 1e3:.1f} ms, wall/step {wall * 1e3:.1f} ms")
         if eng.last_selected is not None:
             S = eng.last_selected.double()

@@ -3,12 +3,15 @@
     python -m tread_amd.kernel_bench assemble  [--workload qwen2.5-7b-32k] [--iters 20]
     python -m tread_amd.kernel_bench attention [--workload qwen2.5-7b-32k] [--shape recompute|prefill|query]
     python -m tread_amd.kernel_bench copy      [--workload qwen2.5-7b-32k]
+    python -m tread_amd.kernel_bench tiercopy  [--workload qwen2.5-1.5b-16k]
 
 `assemble` launches the fused re-rotate+assemble kernel on one request's blocks (prefix + every
 doc, each doc shifted); `copy` copies the same number of bytes with torch (the calibration for
 HBM traffic counters); `attention` runs the recompute attention kernel on a recompute-shaped row
 set (20% of the doc positions, sorted), a full causal prefill, or the query rows. Each prints its
 time per launch and achieved GB/s or TFLOP/s; under rocprofv3 every launch is one dispatch.
+`tiercopy` moves every block of a request (prefix + docs) from pinned host memory to the GPU the
+way a batch of host-tier promotions does (layer groups, one library call) and reports the DMA time.
 """
 import argparse
 import sys
@@ -63,6 +66,29 @@ def bench_copy(cfg, n_docs, doc_len, n_sys, n_query, iters):
     print(f"copy: {n * 2} bytes read + written, {sec * 1e6:.1f} us, {2 * n * 2 / sec / 1e9:.0f} GB/s")
 
 
+def bench_tiercopy(cfg, n_docs, doc_len, n_sys, n_query, iters):
+    L, kv, hd = cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim
+    lens = [n_sys] + [doc_len] * n_docs
+    host = [torch.empty(L, 1, kv, n, hd, dtype=torch.bfloat16, pin_memory=True) for n in lens for _ in range(2)]
+    dev = [torch.empty_like(t, device="cuda") for t in host]
+    s = torch.cuda.Stream()
+    groups = _hip.layer_groups(L)
+    nbytes = sum(t.numel() * t.element_size() for t in host)
+    times = []
+    for _ in range(iters + 1):
+        ev = [torch.cuda.Event() for _ in groups]
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        _hip.copy_layers(dev, host, s, groups, ev)
+        e1.record(s)
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) / 1e3)
+    sec = sorted(times[1:])[len(times[1:]) // 2]
+    print(f"tiercopy: {len(lens)} blocks, {nbytes} bytes in {len(groups)} layer groups ({len(groups) * len(host)} DMAs): "
+          f"{sec * 1e3:.2f} ms, {nbytes / sec / 1e9:.1f} GB/s")
+
+
 def bench_attention(cfg, n_docs, doc_len, n_sys, n_query, iters, shape, ratio=0.2):
     hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     T = n_sys + n_docs * doc_len
@@ -91,7 +117,7 @@ def bench_attention(cfg, n_docs, doc_len, n_sys, n_query, iters, shape, ratio=0.
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("kernel", choices=["assemble", "copy", "attention"])
+    ap.add_argument("kernel", choices=["assemble", "copy", "attention", "tiercopy"])
     ap.add_argument("--workload", default="qwen2.5-7b-32k", choices=list(WORKLOADS))
     ap.add_argument("--shape", default="recompute", choices=["recompute", "prefill", "query"])
     ap.add_argument("--iters", type=int, default=20)
@@ -103,6 +129,8 @@ def main(argv=None):
         bench_assemble(cfg, n_docs, doc_len, n_sys, n_query, args.iters)
     elif args.kernel == "copy":
         bench_copy(cfg, n_docs, doc_len, n_sys, n_query, args.iters)
+    elif args.kernel == "tiercopy":
+        bench_tiercopy(cfg, n_docs, doc_len, n_sys, n_query, min(args.iters, 5))
     else:
         bench_attention(cfg, n_docs, doc_len, n_sys, n_query, args.iters, args.shape)
     return 0
