@@ -2,18 +2,24 @@
 //
 // Rows are (query token, query head) pairs of one KV head group: row r of KV head h is token
 // r / G, query head h*G + r % G (G = hq / hkv), so the G heads that share a KV head share every
-// K/V tile staged in LDS (GQA in-kernel, no repeat_kv). A work group of 8 waves owns 256 rows
-// (ATT_QB 32-row query blocks per wave; one fits the register file best, 198 VGPRs and two waves
-// per SIMD) and each wave computes the transposed score blocks S^T = K Q^T, so that after the
-// softmax its probabilities already sit in the B-operand layout of O^T = V^T P^T: every lane
-// holds one query column for both products, and the online-softmax rescale is a per-lane scalar.
+// K/V tile staged in LDS (GQA in-kernel, no repeat_kv). A work group of 8 waves owns 256 rows (32
+// per wave, two waves per SIMD) and each wave computes the transposed score blocks S^T = K Q^T, so
+// that after the softmax its probabilities already sit in the B-operand layout of O^T = V^T P^T:
+// every lane holds one query column for both products, and the online-softmax rescale is a
+// per-lane scalar. Q is pre-multiplied by scale * log2(e) and the score MFMAs start from -m (the
+// running max), so they produce the exponent of exp2 directly. The online softmax keeps a stale
+// row max until it is 2^8 too small, so the O rescale runs a handful of times per row, not per
+// tile.
+//
 // K and V tiles go from global memory straight into LDS (no register staging), row-major
-// [key][d] with XOR-swizzled chunks; the A operand of the PV product (V^T) is read with gfx950's
-// transposing LDS read, two 8-byte reads per lane and fragment. Tiles are
-// double-buffered in LDS with one barrier per 64-key tile. The online softmax keeps a stale row
-// max until it is 2^8 too small, so the O rescale runs a handful of times per row, not per tile. The key range of a work group is the union of [0, n_shared) and
-// [min kseg, max kend]; the visibility predicate (key <= kend[row] and key outside the row's
-// masked gap) is evaluated in registers only on tiles that cross a row's boundary.
+// [key][d] with XOR-swizzled chunks, three tile buffers deep; the A operand of the PV product
+// (V^T) is read with gfx950's transposing LDS read. Fragment reads are inline asm with explicit
+// waits, streaming ahead of the MFMAs. One step per 64-key tile: an MFMA phase (scores of the next
+// tile, then the PV product of this one) and a softmax phase (mask, row max, rescale,
+// exponentials), which the two waves sharing a SIMD run in opposite order (ping-pong). The key
+// range of a work group is the union of [0, n_shared) and [min kseg, max kend]; the visibility
+// predicate (key <= kend[row] and key outside the row's masked gap) is evaluated in registers only
+// on tiles that cross a row's boundary.
 //
 // Work groups are mapped XCD-aware: the hardware deals work group ids round-robin over the 8
 // XCDs, so ids are remapped such that every XCD works on one KV head at a time, longest row tiles
@@ -257,7 +263,9 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   const int nB = endB > startB ? (endB - startB + ATT_BK - 1) / ATT_BK : 0;
   const int ntiles = nA + nB;
 
-  // ---- Q^T fragments (B operand), resident for the whole kernel
+  // ---- Q^T fragments (B operand), resident for the whole kernel, pre-multiplied by
+  // scale * log2(e) (rounded to bf16, as the reference's math path rounds its scaled q), so that
+  // the MFMA, started from -m_run, yields the exponent of exp2 directly
   bf16x8_t qf[KS];
   {
     const bf16_t* qp = a.q + (qi * a.hq + qh) * HD + half * 8;
@@ -265,6 +273,8 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     for (int s = 0; s < KS; ++s) {
       u32x4_t t = {0, 0, 0, 0};
       if (valid) t = *reinterpret_cast<const u32x4_t*>(qp + s * 16);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) t[w] = pack_bf(lo_bf(t[w]) * a.scale_log2, hi_bf(t[w]) * a.scale_log2);
       qf[s] = __builtin_bit_cast(bf16x8_t, t);
     }
   }
@@ -331,9 +341,12 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
 #pragma unroll
     for (int x = 0; x < 16; ++x) oacc[d][x] = 0.f;
   // running max (log2-scaled units, shared by lanes l and l ^ 32) and this lane's partial sums
-  float m_run = -1e30f;
+  float m_run = 0.f;     // scores arrive as s * scale_log2 - m_run (the MFMA starts from -m_run)
+  bool m_set = false;     // m_run holds a real row max (else 0, and nothing is accumulated yet)
+  f32x16_t mneg;
+#pragma unroll
+  for (int x = 0; x < 16; ++x) mneg[x] = 0.f;
   float lsum[4] = {0.f, 0.f, 0.f, 0.f};
-  const float cs = a.scale_log2;
 
   // this lane's A-operand (K) fragment addresses for the 32-key half 0 of buffer 0, one per
   // k-step: row c, chunk (2 st + half) swizzled; half 1 and the buffers are fixed offsets
@@ -368,8 +381,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       lgkm_wait<k_after>(kf[i]);
       constexpr int kb = i / KS, st = i % KS;
       if constexpr (st == 0) {
-        const f32x16_t z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i], qf[st], z, 0, 0, 0);
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i], qf[st], mneg, 0, 0, 0);
       } else {
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i], qf[st], s[kb], 0, 0, 0);
       }
@@ -380,8 +392,9 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     });
   };
   // visibility mask (tiles crossing a row boundary), row max, lazy rescale of O and the sums:
-  // exponentiate against a stale max m_run and move it only when some row's max outgrew it by
-  // more than 2^8; p then stays <= 256 and the final division by the sum is exact either way
+  // the scores arrive relative to a stale max m_run and move (with O and the sums) only when some
+  // row's max outgrew it by more than 2^8, or on a row's first visible keys; p then stays <= 256
+  // and the final division by the sum is exact either way
   auto settle = [&](int j, f32x16_t (&s)[2]) {
     int s0, s1;
     tile_bounds(j, s0, s1);
@@ -406,27 +419,34 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       mx[q] = fmaxf(mx[q], s[1][q + 12]);
     }
     const float tmax = xhalf_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])));
-    const float m_cand = fmaxf(m_run, tmax * cs);
-    if (__ballot(m_cand > m_run + ATT_RESCALE_LOG2)) {
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_cand);
+    const bool need = m_set ? tmax > ATT_RESCALE_LOG2 : tmax > -INFINITY;
+    if (__ballot(need)) {
+      const float sh = need ? tmax : 0.f;
+      const float corr = __builtin_amdgcn_exp2f(-sh);
 #pragma unroll
       for (int q = 0; q < 4; ++q) lsum[q] *= corr;
 #pragma unroll
       for (int d = 0; d < DB; ++d)
 #pragma unroll
         for (int x = 0; x < 16; ++x) oacc[d][x] *= corr;
-      m_run = m_cand;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) s[kb][x] -= sh;
+      m_run += sh;
+      m_set = m_set || need;
+#pragma unroll
+      for (int x = 0; x < 16; ++x) mneg[x] = -m_run;
     }
   };
-  // P = exp2(S * scale - m) as the B operand of the 4 PV k-steps (16 keys each); register x of
-  // s[kb] feeds k-step kb * 2 + x / 8
+  // P = exp2(S') (S' = s * scale * log2(e) - m) as the B operand of the 4 PV k-steps (16 keys
+  // each); register x of s[kb] feeds k-step kb * 2 + x / 8
   auto to_p = [&](f32x16_t (&s)[2], bf16x8_t (&pb)[4]) {
-    const float mu = m_run;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int x = 0; x < 16; ++x) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][x], cs, -mu));
+        const float p = __builtin_amdgcn_exp2f(s[kb][x]);
         s[kb][x] = p;
         lsum[x & 3] += p;
       }
@@ -588,7 +608,8 @@ __global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(const AttnArg
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   // global max of the split maxima
   float m = -INFINITY;
-  for (int s = t; s < a.nsplit; s += CMB_THREADS) m = fmaxf(m, a.ws_ml[(p0 + s * stride) * 2]);
+  for (int s = t; s < a.nsplit; s += CMB_THREADS)
+    if (a.ws_ml[(p0 + s * stride) * 2 + 1] > 0.f) m = fmaxf(m, a.ws_ml[(p0 + s * stride) * 2]);
   m = wave_max_f(m);
   if (lane == 0) red[wv] = m;
   __syncthreads();
