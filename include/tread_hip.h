@@ -89,7 +89,8 @@ int tread_dev_score_bf16(const void* k_src, const void* v_src, int64_t ld, const
  * order to sel_out (int64 [k]). Among equal scores at the threshold the lowest indices win.
  * Replaces tread/blend.py:160-169 (dev.topk(budget).indices, all_c[top], S.sort()): since the
  * candidate positions are ascending, ascending indices give S already sorted.
- * Scratch: ws of at least tread_topk_workspace_bytes(n) bytes (device).
+ * n <= 2^20 candidates (TREAD_ERANGE above). Scratch: ws of at least tread_topk_workspace_bytes(n)
+ * bytes (device; 0 today: the selection runs in one work group out of LDS).
  */
 size_t tread_topk_workspace_bytes(int64_t n);
 int tread_topk_select_bf16(const void* score, int64_t n, int64_t k, int64_t* sel_out, void* ws, size_t ws_bytes,

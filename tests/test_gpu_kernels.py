@@ -203,7 +203,8 @@ def _brute_topk(score, k):
     return sorted(order[:k])
 
 
-@pytest.mark.parametrize("n,k", [(1, 1), (10, 0), (10, 10), (1000, 200), (32000, 6400), (32000, 16000), (40000, 1)])
+@pytest.mark.parametrize("n,k", [(1, 1), (10, 0), (10, 10), (1000, 200), (32000, 6400), (32000, 16000), (40000, 1),
+                                 (65536, 13107), (65537, 13107), (100000, 20000)])
 def test_topk_select_equals_brute_force(n, k):
     g = torch.Generator().manual_seed(n + k)
     # few distinct bf16 values => many ties at the threshold

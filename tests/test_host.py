@@ -47,6 +47,9 @@ def test_error_paths_are_reported_without_a_gpu():
     assert rc != 0 and b"bad shape" in lib.tread_last_error()
     rc = lib.tread_topk_select_bf16(None, 10, 11, None, None, 0, None)
     assert rc != 0 and b"outside" in lib.tread_last_error()
+    fake = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
+    rc = lib.tread_topk_select_bf16(fake, (1 << 20) + 1, 10, fake, None, 0, None)
+    assert rc != 0 and b"above" in lib.tread_last_error()
     rc = lib.tread_rope_assemble_bf16(None, 1, None, None, 2, 2, 10, 128, None, 0, 2, None)
     assert rc != 0
     assert lib.tread_topk_workspace_bytes(1000) == 0

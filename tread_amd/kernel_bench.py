@@ -4,6 +4,7 @@
     python -m tread_amd.kernel_bench attention [--workload qwen2.5-7b-32k] [--shape recompute|prefill|query]
     python -m tread_amd.kernel_bench copy      [--workload qwen2.5-7b-32k]
     python -m tread_amd.kernel_bench tiercopy  [--workload qwen2.5-1.5b-16k]
+    python -m tread_amd.kernel_bench deviation [--workload qwen2.5-7b-32k]
 
 `assemble` launches the fused re-rotate+assemble kernel on one request's blocks (prefix + every
 doc, each doc shifted); `copy` copies the same number of bytes with torch (the calibration for
@@ -12,6 +13,8 @@ set (20% of the doc positions, sorted), a full causal prefill, or the query rows
 time per launch and achieved GB/s or TFLOP/s; under rocprofv3 every launch is one dispatch.
 `tiercopy` moves every block of a request (prefix + docs) from pinned host memory to the GPU the
 way a batch of host-tier promotions does (layer groups, one library call) and reports the DMA time.
+`deviation` scores every doc position of a request (fresh layer-1 k/v rows of a qkv GEMM output
+against the assembled layer-1 cache) and selects the top 20% of them, each launch timed alone.
 """
 import argparse
 import sys
@@ -115,9 +118,32 @@ def bench_attention(cfg, n_docs, doc_len, n_sys, n_query, iters, shape, ratio=0.
           f"{flop / sec / 1e12:.1f} TFLOP/s")
 
 
+def bench_deviation(cfg, n_docs, doc_len, n_sys, n_query, iters, ratio=0.2):
+    hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    T = n_sys + n_docs * doc_len
+    n = n_docs * doc_len
+    ld = (hq + 2 * hkv) * hd  # one row of the fused qkv projection output
+    qkv = torch.randn(n, ld, device="cuda", dtype=torch.bfloat16)
+    pos = torch.arange(n_sys, T, device="cuda")
+    ang = pos[:, None].float() * inv_freq_of(cfg).cuda()[None, :]
+    cos, sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+    K = torch.randn(1, hkv, T + n_query, hd, device="cuda", dtype=torch.bfloat16)
+    V = torch.randn_like(K)
+    score = torch.empty(n, device="cuda", dtype=torch.bfloat16)
+    k = int(round(ratio * n))
+    sel = torch.empty(k, device="cuda", dtype=torch.int64)
+    kc = hq * hd
+    t_score = _timed(lambda: _hip.dev_score(qkv, cos, sin, pos, hkv, hd, K, V, k_col=kc, out=score), iters)
+    t_sel = _timed(lambda: _hip.topk_select(score, k, out=sel), iters)
+    nbytes = n * 4 * hkv * hd * 2  # fresh k, v + gathered cache rows
+    print(f"dev_score: {n} candidates, {nbytes} algorithmic bytes, {t_score * 1e6:.1f} us, "
+          f"{nbytes / t_score / 1e9:.0f} GB/s")
+    print(f"topk_select: top {k} of {n}: {t_sel * 1e6:.1f} us")
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("kernel", choices=["assemble", "copy", "attention", "tiercopy"])
+    ap.add_argument("kernel", choices=["assemble", "copy", "attention", "tiercopy", "deviation"])
     ap.add_argument("--workload", default="qwen2.5-7b-32k", choices=list(WORKLOADS))
     ap.add_argument("--shape", default="recompute", choices=["recompute", "prefill", "query"])
     ap.add_argument("--iters", type=int, default=20)
@@ -131,6 +157,8 @@ def main(argv=None):
         bench_copy(cfg, n_docs, doc_len, n_sys, n_query, args.iters)
     elif args.kernel == "tiercopy":
         bench_tiercopy(cfg, n_docs, doc_len, n_sys, n_query, min(args.iters, 5))
+    elif args.kernel == "deviation":
+        bench_deviation(cfg, n_docs, doc_len, n_sys, n_query, args.iters)
     else:
         bench_attention(cfg, n_docs, doc_len, n_sys, n_query, args.iters, args.shape)
     return 0
