@@ -95,6 +95,37 @@ def time_assemble(eng, system, docs, order, n_query, iters=20):
     return sec, nbytes
 
 
+def time_decode(eng, system, docs, query, ratio, n):
+    """n greedy decode steps after a reuse prefill, synchronising on every token as the reference
+    server's loop does (tread/server.py:201-208). Bytes per step: every weight of the layers, the
+    final norm and lm_head, plus the K and V rows each step attends to (one embedding row aside)."""
+    P = eng.P
+    wbytes = sum(t.numel() * t.element_size() for lw in P.layers for t in vars(lw).values()
+                 if isinstance(t, torch.Tensor))
+    wbytes += sum(t.numel() * t.element_size() for t in (P.norm, P.lm_head))
+    logits, cache, _ = eng.prefill(system, docs, query, ratio=ratio, reserve=n)
+    nxt = logits.argmax()
+    int(nxt)
+    for _ in range(2):  # first steps capture the decode graph
+        nxt = eng.decode(cache, nxt.view(1)).argmax()
+        int(nxt)
+    T0 = cache.length
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n):
+        nxt = eng.decode(cache, nxt.view(1)).argmax()
+        int(nxt)
+    sec = (time.perf_counter() - t0) / n
+    kv = 2 * P.L * P.hkv * P.hd * 2 * (T0 + (n + 1) / 2)  # mean keys attended per step
+    step_bytes = wbytes + kv
+    gbs = step_bytes / sec / 1e9
+    log(f"[bench] decode: {sec * 1e3:.3f} ms/token over {n} tokens at {T0} context rows, "
+        f"{step_bytes / 1e9:.2f} GB per step ({wbytes / 1e9:.2f} GB weights), {gbs:.0f} GB/s")
+    return {"tokens": n, "context_rows": T0, "ms_per_token": round(sec * 1e3, 3), "bytes_per_token": int(step_bytes),
+            "achieved_gbs": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "graph": cache.graph is not None}
+
+
 def cpu_baseline(preset_name, n_docs, doc_len, n_sys, n_query, ratio, threads):
     """The oracle (the reference's torch path restated on the CPU, bf16) timed on a bounded sample
     of the same workload and extrapolated to one request's TTFT:
@@ -188,6 +219,8 @@ def main():
     ap.add_argument("--full-reps", type=int, default=3, help="full-prefill reps for the TTFT denominator (0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode", type=int, default=32,
+                    help="greedy decode steps timed after the TTFT loop on the last request's cache (0: skip)")
     ap.add_argument("--gpu-tier-docs", type=int, default=None,
                     help="doc blocks the GPU tier holds (default: the workload's setting; -1: all)")
     ap.add_argument("--no-tune", action="store_true",
@@ -276,6 +309,7 @@ def main():
         sec, nbytes = time_assemble(eng, system, docs, perm, n_query)
         gbs = nbytes / sec / 1e9
         log(f"[bench] assemble: {sec * 1e6:.1f} us, {gbs:.0f} GB/s")
+        decode = time_decode(eng, system, order, query, args.ratio, args.decode) if args.decode > 0 else None
     ttft_ms = statistics.median(ttfts) * 1e3
     med = {k: round(statistics.median(s[k] for s in stages) * 1e3, 2) for k in stages[0]}
     cpu = None
@@ -309,6 +343,7 @@ def main():
                      "traffic": MEASURED_ASSEMBLE_TRAFFIC.get(args.workload), "avg_us": round(sec * 1e6, 2),
                      "algorithmic_bytes": nbytes},
         "cpu_baseline": cpu,
+        "decode": decode,
     }
     print(json.dumps(out), flush=True)
 

@@ -390,6 +390,29 @@ def prefill_full(m, prefix_ids, docs, query_ids):
     return M.logits_last(m, h), (K, V), st
 
 
+def generate_greedy(m, logits, K, V, max_tokens, eos_ids=(), forced=None):
+    """tread/server.py:194-210, the greedy loop after `engine.prefill`: next = argmax(logits); stop
+    on an eos id or after max_tokens tokens; every emitted token is run through the model on top
+    of the cache (the reference's DynamicCache path, concatenating K/V) to give the next logits.
+    `forced` (a token list) replaces the argmax picks, so another implementation's tokens can be
+    replayed step by step (test hook, not reference behaviour).
+    Returns (tokens, finish_reason, per-step logits [logits of the prompt, then one per token])."""
+    out, steps = [], [logits]
+    reason = "stop"
+    while True:
+        nxt = int(logits.argmax()) if forced is None else forced[len(out)] if len(out) < len(forced) else None
+        if nxt is None or nxt in eos_ids:
+            break
+        if len(out) >= max_tokens:
+            reason = "length"
+            break
+        out.append(nxt)
+        h, K, V = M.forward(m, torch.tensor([nxt]), past=(K, V))
+        logits = M.logits_last(m, h)
+        steps.append(logits)
+    return out, reason, steps
+
+
 def kl(a, b):
     """tests/test_engine.py:42-43."""
     import torch.nn.functional as F

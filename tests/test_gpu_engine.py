@@ -355,3 +355,92 @@ def test_empty_docs_and_zero_budget(setup):
     _, docs, _ = request(cfg, seed=12, n_docs=1, lens=(3,))
     _, _, st = eng.prefill(on(prefix), on(docs), on(query), ratio=0.1)  # round(0.3) == 0
     assert st.recompute_eff == 0.0
+
+
+def _decode_steps(eng, prefix, docs, query, n, ratio, reserve=None, grow=False):
+    """Prefill, then n greedy decode steps; returns (tokens, per-step logits incl. the prompt's)."""
+    logits, cache, _ = eng.prefill(on(prefix), on(docs), on(query), ratio=ratio, policy="boundary",
+                                   reserve=n if reserve is None else reserve)
+    if grow:
+        cache.grow(cache.capacity + 7)
+    toks, steps = [], [logits]
+    for _ in range(n):
+        toks.append(int(steps[-1].argmax()))
+        steps.append(eng.decode(cache, torch.tensor([toks[-1]], device=DEV)))
+    return toks, steps, cache
+
+
+@pytest.mark.parametrize("graphs,ratio,reserve,grow", [(False, 0.0, None, False), (False, 0.3, 0, False),
+                                                      (True, 0.3, None, False), (True, 0.3, None, True)])
+def test_decode_matches_oracle_generation_step_by_step(setup, graphs, ratio, reserve, grow):
+    """tread/server.py:194-210: the decode steps after a reuse prefill, replayed through the
+    oracle's loop with the same tokens (same recompute rows), give per-step logits no further from
+    the fp32 truth than the reference's own bf16 path is (the first-token bar above); every token
+    is the truth's argmax unless its top two are a near-tie. Covers the eager step, growth of a
+    cache with no room left, the graph step, and a graph bucket's cache that was moved (then
+    stepped eagerly)."""
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=13)
+    eng = Engine(gpu, BlockStore(1 << 30), graphs=graphs)
+    if graphs:
+        eng.prefill(on(prefix), on(docs), on(query))  # fill the store: the request below hits
+    n = 6
+    toks, steps, cache = _decode_steps(eng, prefix, docs, query, n, ratio, reserve, grow)
+    assert cache.length == sum(map(len, docs)) + len(prefix) + len(query) + n
+    assert (cache.graph is not None) == (graphs and not grow)
+    runs = []
+    for m in (ref, fp32_oracle(cfg, ref)):
+        oeng = R.Engine(m, R.BlockStore(1 << 30))
+        ologits, (K, V), _ = oeng.prefill(prefix, docs, query, ratio=ratio, policy="boundary")
+        otoks, _, osteps = R.generate_greedy(m, ologits, K, V, max_tokens=n, forced=toks)
+        assert otoks == toks and len(osteps) == n + 1
+        runs.append(osteps)
+    for i, (b, c) in enumerate(zip(*runs)):
+        assert kl(c, steps[i]) <= 2 * kl(c, b) + 1e-5, (i, kl(c, steps[i]), kl(c, b))
+        if i < n:
+            top2 = c.float().topk(2).values
+            if (top2[0] - top2[1]).item() > 0.05:
+                assert toks[i] == int(c.argmax())
+
+
+@pytest.mark.parametrize("name", list(CFGS))
+def test_decode_within_kl_1e4_at_benchmark_init(name):
+    """The north-star bar on every decode step at the benchmark's N(0, 0.02) weights:
+    KL(reference bf16, ours) < 1e-4 (graph steps after a 20% recompute)."""
+    cfg, gpu, ref = build(name, std=0.02)
+    prefix, docs, query = request(cfg, seed=22)
+    eng = Engine(gpu, BlockStore(1 << 30), graphs=True)
+    eng.prefill(on(prefix), on(docs), on(query))
+    toks, steps, cache = _decode_steps(eng, prefix, docs, query, 6, 0.2)
+    assert cache.graph is not None
+    oeng = R.Engine(ref, R.BlockStore(1 << 30))
+    ologits, (K, V), _ = oeng.prefill(prefix, docs, query, ratio=0.2, policy="boundary")
+    _, _, osteps = R.generate_greedy(ref, ologits, K, V, max_tokens=6, forced=toks)
+    for i, (b, a) in enumerate(zip(osteps, steps)):
+        assert kl(b, a) < 1e-4, (i, kl(b, a))
+
+
+def test_graph_decode_equals_eager_decode_and_generate_stops_like_the_reference(setup):
+    """The graph step (padded rows) and the eager step give the same logits; Engine.generate's
+    stop rules (eos id, max_tokens) cut where tread/server.py:200-206 does, with the same tokens
+    as the step-by-step loop. One decode graph is captured and replayed by later steps."""
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=14)
+    eager = Engine(gpu, BlockStore(1 << 30))
+    graphed = Engine(gpu, BlockStore(1 << 30), graphs=True)
+    for e in (eager, graphed):
+        e.prefill(on(prefix), on(docs), on(query))
+    ta, sa, _ = _decode_steps(eager, prefix, docs, query, 5, 0.3)
+    tb, sb, _ = _decode_steps(graphed, prefix, docs, query, 5, 0.3)
+    for a, b in zip(sa, sb):
+        assert kl(a, b) < 1e-5
+    assert graphed.runner.captures == 3  # recompute loop, query forward, one decode step
+    toks, reason, st, cache = eager.generate(on(prefix), on(docs), on(query), max_tokens=5, ratio=0.3,
+                                             policy="boundary")
+    assert (toks, reason) == (ta, "length") and st.hits == 1 + len(docs)
+    j = ta.index(ta[3])
+    toks, reason, _, _ = eager.generate(on(prefix), on(docs), on(query), max_tokens=5, eos_ids=[ta[3]], ratio=0.3,
+                                        policy="boundary")
+    assert (toks, reason) == (ta[:j], "stop")
+    toks, reason, _, _ = eager.generate(on(prefix), on(docs), on(query), max_tokens=0, ratio=0.3, policy="boundary")
+    assert (toks, reason) == ([], "length")

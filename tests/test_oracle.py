@@ -293,6 +293,30 @@ def test_full_recompute_matches_full_prefill(om):
     assert kl(ref, out2) < 1e-5 and st.tokens_prefilled == len(prefix) + sum(map(len, docs))
 
 
+def test_greedy_generation_steps_equal_full_forward_of_the_extended_sequence(om):
+    """tread/server.py:194-210 restated: every step's logits (incremental, on the cache) equal a
+    fresh full forward over the prompt plus the tokens emitted so far; the stop rules (eos id,
+    max_tokens) cut the token list where the reference's loop does."""
+    cfg, m = om
+    prefix, docs, query = _req(cfg)
+    logits, (K, V), _ = R.prefill_full(m, prefix, docs, query)
+    toks, reason, steps = R.generate_greedy(m, logits, K, V, max_tokens=5)
+    assert reason == "length" and len(toks) == 5 and len(steps) == 6
+    for i in range(6):
+        ext = torch.cat([query, torch.tensor(toks[:i], dtype=torch.long)])
+        full, _, _ = R.prefill_full(m, prefix, docs, ext)
+        assert kl(full, steps[i]) < 1e-6
+        if i < 5:
+            assert toks[i] == int(full.argmax())
+    j = toks.index(toks[2])
+    t2, r2, _ = R.generate_greedy(m, logits, K, V, max_tokens=5, eos_ids={toks[2]})
+    assert (t2, r2) == (toks[:j], "stop")
+    assert R.generate_greedy(m, logits, K, V, max_tokens=0)[:2] == ([], "length")
+    forced = [(t + 1) % cfg.vocab_size for t in toks[:3]]
+    t4, r4, s4 = R.generate_greedy(m, logits, K, V, max_tokens=5, forced=forced)
+    assert t4 == forced and len(s4) == 4
+
+
 def test_reordered_request_hits_and_equals_cold_assembly(om):
     cfg, m = om
     prefix, docs, query = _req(cfg)

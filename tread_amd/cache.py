@@ -13,8 +13,21 @@ import torch
 
 
 class KVCache:
-    def __init__(self, K, V, length):
+    def __init__(self, K, V, length, graph=None):
         self.K, self.V, self.length = K, V, int(length)
+        self.graph = graph  # the hipGraph bucket whose static buffer this cache is (or None)
+
+    def grow(self, capacity):
+        """Move the valid rows into a new buffer of at least `capacity` rows (decoding past the
+        preallocated room). The cache stops aliasing a graph bucket."""
+        if capacity <= self.capacity:
+            return
+        shape = self.K.shape[:-2] + (capacity, self.K.shape[-1])
+        K = torch.empty(shape, dtype=self.K.dtype, device=self.K.device)
+        V = torch.empty_like(K)
+        K[..., :self.length, :].copy_(self.K[..., :self.length, :])
+        V[..., :self.length, :].copy_(self.V[..., :self.length, :])
+        self.K, self.V, self.graph = K, V, None
 
     @classmethod
     def from_layers(cls, K, V):

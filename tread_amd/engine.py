@@ -159,8 +159,10 @@ class Engine:
         return blocks
 
     @torch.inference_mode()
-    def prefill(self, prefix_ids, docs, query_ids, ratio=0.0, policy="deviation", namespace="", gen=None):
-        """tread/engine.py:98-136. Returns (logits [vocab], KVCache, RequestStats)."""
+    def prefill(self, prefix_ids, docs, query_ids, ratio=0.0, policy="deviation", namespace="", gen=None, reserve=0):
+        """tread/engine.py:98-136. Returns (logits [vocab], KVCache, RequestStats). `reserve`: rows
+        kept free after the query for `decode` (an addition; the reference's cache grows by
+        concatenation)."""
         st = RequestStats()
         self._sync()
         t0 = time.perf_counter()
@@ -177,11 +179,11 @@ class Engine:
             n, budget = select(ratio, docs)
             if budget > 0:
                 start = 1 if policy == "deviation" else 0
-                graph = self.runner.cache_for(start, budget, T, Nq, dev)
+                graph = self.runner.cache_for(start, budget, T, Nq, dev, room=Nq + reserve)
         if graph is not None:
             K, V = graph.K, graph.V
         else:
-            K, V = alloc_cache(self.P, T + Nq, dev)
+            K, V = alloc_cache(self.P, T + Nq + reserve, dev)
         sources = [(pb, 0, 0)]
         cands = []
         offset = Pn
@@ -203,7 +205,7 @@ class Engine:
         t2 = time.perf_counter()
 
         if graph is not None and Nq > 0:
-            logits = self.runner.query(graph, query_ids, T, hook=asm.ensure)
+            logits = self.runner.query(graph, query_ids, T, hook=asm.ensure).clone()  # the graph's output is static
         else:
             R = make_rows(self.P, torch.arange(T, T + Nq, device=dev))
             h, d = run_layers(self.P, embed(self.P, query_ids), None, R, Kl, Vl, range(self.P.L), hook=asm.ensure)
@@ -211,7 +213,54 @@ class Engine:
         self._sync()
         t3 = time.perf_counter()
         st.t = dict(assemble=t1 - t0, blend=t2 - t1, query=t3 - t2, ttft=t3 - t0)
-        return logits, KVCache(K, V, T + Nq), st
+        return logits, KVCache(K, V, T + Nq, graph=graph), st
+
+    @torch.inference_mode()
+    def decode(self, cache, ids):
+        """One step of the reference server's generation loop (tread/server.py:201-208:
+        `model(nxt.view(1, 1), past_key_values=cache, use_cache=True, num_logits_to_keep=1)`) on
+        this engine's cache: the token ids' k/v are written in place at rows cache.length.. (no
+        per-layer concatenation) and the last one's logits [vocab] are returned. Replayed from a
+        graph when the cache is a graph bucket with room for the padded rows; a cache without
+        room grows first. A bucket's cache is valid until the next request replays that bucket."""
+        n = ids.numel()
+        T = cache.length
+        if T + n > cache.capacity:
+            cache.grow(T + n + 256)
+        g = cache.graph
+        if g is not None and self.runner is not None and self.runner.fits(g, n, T):
+            logits = self.runner.decode(g, ids, T).clone()
+        else:
+            R = make_rows(self.P, torch.arange(T, T + n, device=ids.device))
+            h, d = run_layers(self.P, embed(self.P, ids), None, R, cache.K.unbind(0), cache.V.unbind(0),
+                              range(self.P.L))
+            logits = final_logits(self.P, h, d)
+        cache.length = T + n
+        return logits
+
+    @torch.inference_mode()
+    def generate(self, prefix_ids, docs, query_ids, max_tokens=16, eos_ids=(), ratio=0.0, policy="deviation",
+                 namespace="", max_seconds=None):
+        """The reference server's greedy loop around prefill (tread/server.py:194-210): the next
+        token is the argmax; stop on an eos id ("stop"), after max_tokens tokens ("length") or
+        past max_seconds ("time"); every emitted token goes through `decode`. Returns
+        (tokens, finish_reason, RequestStats, KVCache)."""
+        t0 = time.perf_counter()
+        logits, cache, st = self.prefill(prefix_ids, docs, query_ids, ratio=ratio, policy=policy,
+                                         namespace=namespace, reserve=max_tokens)
+        out, reason = [], "stop"
+        nxt = logits.argmax()
+        eos = set(int(e) for e in eos_ids)
+        while int(nxt) not in eos:
+            if len(out) >= max_tokens:
+                reason = "length"
+                break
+            if max_seconds is not None and time.perf_counter() - t0 > max_seconds:
+                reason = "time"
+                break
+            out.append(int(nxt))
+            nxt = self.decode(cache, nxt.view(1)).argmax()
+        return out, reason, st, cache
 
     @torch.inference_mode()
     def prefill_prefix_only(self, prefix_ids, docs, query_ids):

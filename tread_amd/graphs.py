@@ -151,11 +151,12 @@ class SubsetRunner:
         return g
 
     @torch.inference_mode()
-    def cache_for(self, start, n, T, n_query, device):
+    def cache_for(self, start, n, T, n_query, device, room=None):
         """The bucket graph serving a request that recomputes n rows from layer `start` over a
-        T-row context followed by n_query query rows; its .K/.V are the cache to assemble into.
-        The query forward for n_query rows is captured with it (before anything is assembled)."""
-        g = self._graph(start, n, T, n_query, device)
+        T-row context followed by n_query query rows (and `room` >= n_query rows in all after the
+        context, for decoding); its .K/.V are the cache to assemble into. The query forward for
+        n_query rows is captured with it (before anything is assembled)."""
+        g = self._graph(start, n, T, max(n_query, room or 0), device)
         nq = _q_bucket(n_query)
         if n_query > 0 and nq not in g.queries:
             g.queries[nq] = _QueryGraph(self.P, g, nq, device)
@@ -180,6 +181,22 @@ class SubsetRunner:
         q.last.fill_(n - 1)
         q.graph.replay()
         return q.out
+
+    def fits(self, g, n, T):
+        """Whether n rows appended at row T fit the padded query forward of bucket g."""
+        return T + _q_bucket(n) <= g.t_cap
+
+    @torch.inference_mode()
+    def decode(self, g, ids, T):
+        """One decoding step on bucket g's cache: the query forward for the token ids at rows
+        T.., replayed from a graph (captured on first use for this row bucket; its capture-time
+        rows are the bucket's top rows, which hold no valid cache rows yet or are rewritten
+        before they are read). Returns the last row's logits [vocab]."""
+        nq = _q_bucket(ids.numel())
+        if nq not in g.queries:
+            g.queries[nq] = _QueryGraph(self.P, g, nq, ids.device)
+            self.captures += 1
+        return self.query(g, ids, T)
 
     @torch.inference_mode()
     def run(self, g, h, S, T, hook=None):
