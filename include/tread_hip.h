@@ -23,7 +23,7 @@ typedef void* tread_event_t;  /* hipEvent_t */
 
 /* Thread-local text of the last error (empty string if none). */
 const char* tread_last_error(void);
-/* ABI version of this header; bumps on any signature change. */
+/* ABI version of this header (4); bumps on any signature change. */
 int tread_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------
@@ -122,6 +122,16 @@ int tread_subset_attn_bf16(const void* q, const void* k_cache, const void* v_cac
 int tread_add_rmsnorm_bf16(const void* x, const void* delta, const void* weight, float eps, int64_t n, int hidden,
                            void* sum_out, void* norm_out, tread_stream_t stream);
 int tread_silu_mul_bf16(const void* gate_up, int64_t n, int inter, void* out, tread_stream_t stream);
+
+/* Linear layer of a few token rows (decode steps): y[m, n] = x[m, k] . weight[n, k]^T (+ bias[n]),
+ * bf16, fp32 accumulation, one bf16 rounding (as F.linear). m <= 32; n a multiple of 32; k a
+ * multiple of 128; x rows ldx apart (16-byte aligned), y rows ldy apart; bias may be NULL.
+ * Replaces the q|k|v, o, gate|up, down and lm_head projections (transformers Qwen2Attention /
+ * Qwen2MLP / lm_head) of the decoding step model(nxt.view(1, 1), past_key_values=cache) at
+ * tread/server.py:207, whose GEMMs are weight-streaming.
+ */
+int tread_skinny_linear_bf16(const void* x, int64_t ldx, const void* weight, const void* bias, int64_t m, int64_t n,
+                             int64_t k, void* y, int64_t ldy, tread_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------
  * (d) Block-tier copy: async DMA of `bytes` between pinned host and device memory (either

@@ -173,6 +173,36 @@ def test_silu_mul_vs_torch():
     assert u.max().item() <= 1 and (u == 0).float().mean().item() > 0.99
 
 
+@pytest.mark.parametrize("m,n,k,bias,ldx", [(1, 32, 256, False, 256), (8, 4608, 3584, True, 3584),
+                                             (3, 96, 512, True, 640), (32, 3584, 4608, False, 4608),
+                                             (17, 1024, 4096, False, 4096)])
+def test_skinny_linear_matches_fp32_reference(m, n, k, bias, ldx):
+    """y = x W^T (+ b) of a few rows against the fp32 product of the same bf16 values: within one
+    bf16 ulp of it plus the fp32 reordering error (1e-5 of the sum of |terms|, which matters only
+    where the terms cancel to near zero), and mostly equal to it rounded once."""
+    g = torch.Generator().manual_seed(m * 7 + n)
+    xs = torch.randn(m, ldx, generator=g).to(torch.bfloat16)
+    W = (torch.randn(n, k, generator=g) * 0.05).to(torch.bfloat16)
+    b = torch.randn(n, generator=g).to(torch.bfloat16) if bias else None
+    x = xs[:, :k]
+    ref = x.float() @ W.float().T
+    if bias:
+        ref = ref + b.float()
+    got = _hip.skinny_linear(xs.to(DEV)[:, :k], W.to(DEV), None if b is None else b.to(DEV)).cpu()
+    terms = x.float().abs() @ W.float().abs().T + (b.float().abs() if bias else 0)
+    ulp = 2.0 ** (ref.abs().clamp_min(1e-30).log2().floor() - 7)
+    assert ((got.float() - ref).abs() <= ulp + 1e-5 * terms).all()
+    assert (bf16_ulps(got, ref.to(torch.bfloat16)) == 0).float().mean().item() > 0.95
+
+
+def test_skinny_linear_rejects_unsupported_shapes():
+    x = torch.zeros(33, 256, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        _hip.skinny_linear(x, torch.zeros(32, 256, device=DEV, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        _hip.skinny_linear(x[:4], torch.zeros(48, 256, device=DEV, dtype=torch.bfloat16))
+
+
 # ------------------------------------------------------------------------------------------- (b)
 
 @pytest.mark.parametrize("hd,hkv", [(128, 4), (64, 2), (128, 8)])

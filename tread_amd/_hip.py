@@ -10,7 +10,7 @@ from pathlib import Path
 import torch  # loads torch's HIP runtime first, so the library below binds to the same one
 
 LIB_PATH = Path(__file__).resolve().with_name("libtread_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 c_i64, c_int, c_void, c_float, c_size = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
 P_I64 = ctypes.POINTER(ctypes.c_int64)
@@ -39,6 +39,7 @@ _SIGS = {
                                        c_i64, c_float, c_void, c_void, c_size, c_void]),
     "tread_add_rmsnorm_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_int, c_void, c_void, c_void]),
     "tread_silu_mul_bf16": (c_int, [c_void, c_i64, c_int, c_void, c_void]),
+    "tread_skinny_linear_bf16": (c_int, [c_void, c_i64, c_void, c_void, c_i64, c_i64, c_i64, c_void, c_i64, c_void]),
     "tread_copy_async": (c_int, [c_void, c_void, c_size, c_void, c_void]),
     "tread_copy_layers_async": (c_int, [c_void, c_void, c_void, c_int, c_int, c_void, c_void]),
 }
@@ -187,6 +188,31 @@ def add_rmsnorm(x, weight, eps, delta=None, sum_out=None, norm_out=None):
     _check("tread_add_rmsnorm_bf16", lib().tread_add_rmsnorm_bf16(
         _ptr(x), _ptr(delta), _ptr(weight), float(eps), n, H, _ptr(sum_out), _ptr(norm_out), _stream()))
     return (sum_out if delta is not None else x), norm_out
+
+
+SKINNY_MAX_ROWS = 32
+
+
+def skinny_ok(m, n, k):
+    """Shapes the skinny linear kernel takes (rows <= 32, n % 32 == 0, k % 128 == 0)."""
+    return 0 < m <= SKINNY_MAX_ROWS and n % 32 == 0 and k % 128 == 0
+
+
+def skinny_linear(x, weight, bias=None, out=None):
+    """y = x @ weight.T (+ bias) for a few rows x [m, k] (m <= 32): weight-streaming MFMA kernel."""
+    _need(x, "x", contig=False)
+    _need(weight, "weight")
+    if bias is not None:
+        _need(bias, "bias")
+    m, k = x.shape
+    n = weight.shape[0]
+    if x.stride(1) != 1 or weight.shape[1] != k or not skinny_ok(m, n, k):
+        raise ValueError(f"skinny_linear: unsupported shape x {tuple(x.shape)} weight {tuple(weight.shape)}")
+    if out is None:
+        out = torch.empty(m, n, dtype=x.dtype, device=x.device)
+    _check("tread_skinny_linear_bf16", lib().tread_skinny_linear_bf16(
+        _ptr(x), x.stride(0), _ptr(weight), _ptr(bias), m, n, k, _ptr(out), out.stride(0), _stream()))
+    return out
 
 
 def silu_mul(gate_up, out=None):

@@ -493,6 +493,41 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   // so that after each barrier one of them issues MFMAs while the other exponentiates: the early
   // group settles and exponentiates tile t + 1 after its MFMA phase, the late group tile t before.
   // Each wave's outstanding global loads are whole tiles of LPT instructions.
+  // A wave none of whose 32 rows exists (the last row tile of a group; few query rows) only loads
+  // its share of every tile and meets every barrier of the pipeline below, leaving its SIMD to the
+  // waves with rows.
+  const bool idle = __builtin_amdgcn_readfirstlane(__ballot(valid) == 0ull ? 1 : 0) != 0;
+  if (idle) {
+    if (ntiles > 0) {
+#pragma unroll
+      for (int t = 0; t < ATT_NBUF - 1; ++t)
+        if (t < ntiles) issue_tile(t, t);
+      if constexpr (ATT_NBUF >= 4) {
+        if (ntiles > 2) vm_wait<2 * LPT>();
+        else if (ntiles > 1) vm_wait<LPT>();
+        else vm_wait<0>();
+      } else {
+        if (ntiles > 1) vm_wait<LPT>();
+        else vm_wait<0>();
+      }
+      __syncthreads();
+      int bj = 0;
+      for (int j = 0; j + 1 < ntiles; ++j) {
+        if constexpr (ATT_NBUF >= 4) {
+          if (j + 2 < ntiles) vm_wait<LPT>();
+          else vm_wait<0>();
+        } else {
+          vm_wait<0>();
+        }
+        __syncthreads();
+        const int bn = bj == ATT_NBUF - 1 ? 0 : bj + 1, bprev = bj == 0 ? ATT_NBUF - 1 : bj - 1;
+        const int tl = j + ATT_NBUF - 1;
+        if (tl < ntiles) issue_tile(tl, bprev);
+        bj = bn;
+      }
+    }
+    return;  // no rows: nothing to write
+  }
   if (ntiles > 0) {
 #pragma unroll
     for (int t = 0; t < ATT_NBUF - 1; ++t)

@@ -12,7 +12,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 PKG = HERE.parent
 ROOT = PKG.parent
-SOURCES = ["runtime", "assemble", "deviation", "layer_ops", "attention"]
+SOURCES = ["runtime", "assemble", "deviation", "layer_ops", "attention", "skinny"]
 LIB = PKG / "libtread_hip.so"
 ARCH = os.environ.get("TREAD_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -76,11 +76,20 @@ def run_layers(P, h, delta, R, K, V, layers, kv_only_last=False, hook=None):
     return h, delta
 
 
+def lm_head(P, x):
+    """Logits of the rows x [m, H]. A few rows stream the vocab-sized weight through the skinny
+    linear kernel (measured faster than the library GEMM at m <= 8 on MI355X); more rows use the
+    library GEMM."""
+    if x.shape[0] <= 8 and _hip.skinny_ok(x.shape[0], P.lm_head.shape[0], P.lm_head.shape[1]):
+        return _hip.skinny_linear(x, P.lm_head)
+    return F.linear(x, P.lm_head)
+
+
 def final_logits(P, h, delta):
     """Final RMSNorm + lm_head on the last row only (num_logits_to_keep=1). Returns [vocab]."""
     _, x = _hip.add_rmsnorm(h[-1:].contiguous(), P.norm, P.eps,
                             delta=None if delta is None else delta[-1:].contiguous())
-    return F.linear(x, P.lm_head)[0]
+    return lm_head(P, x)[0]
 
 
 def embed(P, ids):

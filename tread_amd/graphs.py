@@ -16,10 +16,9 @@ host-tier copies only right before that layer: the block-tier DMAs overlap the r
 from collections import OrderedDict
 
 import torch
-import torch.nn.functional as F
 
 from tread_amd import _hip
-from tread_amd.forward import alloc_cache, embed, make_rows, run_layers
+from tread_amd.forward import alloc_cache, embed, lm_head, make_rows, run_layers
 
 
 def _bucket(n, T, n_min=64, n_step=256, t_step=1024):
@@ -74,7 +73,7 @@ class _QueryGraph:
             R = make_rows(P, self.pos)
             h, d = run_layers(P, embed(P, self.ids), None, R, g.Kl, g.Vl, range(P.L))
             _, x = _hip.add_rmsnorm(h.index_select(0, self.last), P.norm, P.eps, delta=d.index_select(0, self.last))
-            return F.linear(x, P.lm_head)[0]
+            return lm_head(P, x)[0]
 
         self.graph, self.out = _capture(body, device)
 

@@ -5,6 +5,7 @@
     python -m tread_amd.kernel_bench copy      [--workload qwen2.5-7b-32k]
     python -m tread_amd.kernel_bench tiercopy  [--workload qwen2.5-1.5b-16k]
     python -m tread_amd.kernel_bench deviation [--workload qwen2.5-7b-32k]
+    python -m tread_amd.kernel_bench skinny    [--workload qwen2.5-7b-32k]
 
 `assemble` launches the fused re-rotate+assemble kernel on one request's blocks (prefix + every
 doc, each doc shifted); `copy` copies the same number of bytes with torch (the calibration for
@@ -15,6 +16,9 @@ time per launch and achieved GB/s or TFLOP/s; under rocprofv3 every launch is on
 way a batch of host-tier promotions does (layer groups, one library call) and reports the DMA time.
 `deviation` scores every doc position of a request (fresh layer-1 k/v rows of a qkv GEMM output
 against the assembled layer-1 cache) and selects the top 20% of them, each launch timed alone.
+`skinny` runs the projections of a decoding step (q|k|v with bias, o, gate|up, down, lm_head) for
+1, 8 and 32 token rows through the skinny-linear kernel and through torch's GEMM, and reports the
+weight-streaming bandwidth of each.
 """
 import argparse
 import sys
@@ -123,17 +127,25 @@ def bench_deviation(cfg, n_docs, doc_len, n_sys, n_query, iters, ratio=0.2):
     T = n_sys + n_docs * doc_len
     n = n_docs * doc_len
     ld = (hq + 2 * hkv) * hd  # one row of the fused qkv projection output
-    qkv = torch.randn(n, ld, device="cuda", dtype=torch.bfloat16)
     pos = torch.arange(n_sys, T, device="cuda")
     ang = pos[:, None].float() * inv_freq_of(cfg).cuda()[None, :]
     cos, sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
-    K = torch.randn(1, hkv, T + n_query, hd, device="cuda", dtype=torch.bfloat16)
-    V = torch.randn_like(K)
+    # four input sets (>= 1 GiB in all), used in turn, so that a launch reads HBM rather than the
+    # 256 MB last-level cache that the previous launch filled
+    sets = [(torch.randn(n, ld, device="cuda", dtype=torch.bfloat16),
+             torch.randn(1, hkv, T + n_query, hd, device="cuda", dtype=torch.bfloat16),
+             torch.randn(1, hkv, T + n_query, hd, device="cuda", dtype=torch.bfloat16)) for _ in range(4)]
     score = torch.empty(n, device="cuda", dtype=torch.bfloat16)
     k = int(round(ratio * n))
     sel = torch.empty(k, device="cuda", dtype=torch.int64)
     kc = hq * hd
-    t_score = _timed(lambda: _hip.dev_score(qkv, cos, sin, pos, hkv, hd, K, V, k_col=kc, out=score), iters)
+    it = iter(range(1 << 30))
+
+    def score_once():
+        qkv, K, V = sets[next(it) % len(sets)]
+        _hip.dev_score(qkv, cos, sin, pos, hkv, hd, K, V, k_col=kc, out=score)
+
+    t_score = _timed(score_once, iters)
     t_sel = _timed(lambda: _hip.topk_select(score, k, out=sel), iters)
     nbytes = n * 4 * hkv * hd * 2  # fresh k, v + gathered cache rows
     print(f"dev_score: {n} candidates, {nbytes} algorithmic bytes, {t_score * 1e6:.1f} us, "
@@ -141,9 +153,32 @@ def bench_deviation(cfg, n_docs, doc_len, n_sys, n_query, iters, ratio=0.2):
     print(f"topk_select: top {k} of {n}: {t_sel * 1e6:.1f} us")
 
 
+def bench_skinny(cfg, iters):
+    import torch.nn.functional as F
+    H, I, hq, hkv, hd = (cfg.hidden_size, cfg.intermediate_size, cfg.num_attention_heads, cfg.num_key_value_heads,
+                         cfg.head_dim)
+    shapes = [("qkv", (hq + 2 * hkv) * hd, H, True), ("o", H, hq * hd, False), ("gate_up", 2 * I, H, False),
+              ("down", H, I, False), ("lm_head", cfg.vocab_size, H, False)]
+    for name, n, k, has_bias in shapes:
+        # enough weight copies (>= 1 GiB) that each launch streams its weight from HBM, as in a
+        # decoding step, not from the 256 MB last-level cache
+        copies = max(2, -(-(1 << 30) // (n * k * 2)))
+        Ws = [torch.randn(n, k, device="cuda", dtype=torch.bfloat16) * 0.02 for _ in range(copies)]
+        b = torch.randn(n, device="cuda", dtype=torch.bfloat16) if has_bias else None
+        for m in (1, 8, 32):
+            x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+            ok = _hip.skinny_ok(m, n, k)
+            it = iter(range(1 << 30))
+            t_s = _timed(lambda: _hip.skinny_linear(x, Ws[next(it) % copies], b), iters) if ok else float("nan")
+            t_t = _timed(lambda: F.linear(x, Ws[next(it) % copies], b), iters)
+            nbytes = n * k * 2
+            print(f"skinny {name} [{m} x {k}] x [{n} x {k}]^T: kernel {t_s * 1e6:.1f} us "
+                  f"({nbytes / t_s / 1e9:.0f} GB/s), torch {t_t * 1e6:.1f} us ({nbytes / t_t / 1e9:.0f} GB/s)")
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("kernel", choices=["assemble", "copy", "attention", "tiercopy", "deviation"])
+    ap.add_argument("kernel", choices=["assemble", "copy", "attention", "tiercopy", "deviation", "skinny"])
     ap.add_argument("--workload", default="qwen2.5-7b-32k", choices=list(WORKLOADS))
     ap.add_argument("--shape", default="recompute", choices=["recompute", "prefill", "query"])
     ap.add_argument("--iters", type=int, default=20)
@@ -157,6 +192,8 @@ def main(argv=None):
         bench_copy(cfg, n_docs, doc_len, n_sys, n_query, args.iters)
     elif args.kernel == "tiercopy":
         bench_tiercopy(cfg, n_docs, doc_len, n_sys, n_query, min(args.iters, 5))
+    elif args.kernel == "skinny":
+        bench_skinny(cfg, args.iters)
     elif args.kernel == "deviation":
         bench_deviation(cfg, n_docs, doc_len, n_sys, n_query, args.iters)
     else:
