@@ -67,8 +67,14 @@ def time_assemble(eng, system, docs, order, n_query, iters=20):
     P = eng.P
     dev = system.device
 
-    def on_gpu(key):  # blocks of either tier; host-tier ones are copied up for this measurement
-        b = eng.store.blocks.get(key) or eng.store.cpu_blocks[key]
+    def on_gpu(key):  # blocks of any tier; host- and disk-tier ones are copied up for this measurement
+        b = eng.store.blocks.get(key) or eng.store.cpu_blocks.get(key)
+        if b is None:
+            from types import SimpleNamespace
+            from tread_amd import blockfile
+            eng.store.drain()
+            K, V, h = blockfile.read_block(eng.store.disk_blocks[key].path)
+            return SimpleNamespace(n_tokens=h["n_tokens"], base=h["base"]), K.to(dev), V.to(dev)
         return b, b.K.to(dev), b.V.to(dev)
 
     pkey = block_key(*eng.sig, "", "prefix", system)
@@ -223,6 +229,9 @@ def main():
                     help="greedy decode steps timed after the TTFT loop on the last request's cache (0: skip)")
     ap.add_argument("--gpu-tier-docs", type=int, default=None,
                     help="doc blocks the GPU tier holds (default: the workload's setting; -1: all)")
+    ap.add_argument("--disk-tier", default=None, metavar="DIR",
+                    help="blocks outside the GPU tier live as files in DIR (no host tier): each request "
+                         "reads them back (from the page cache once written)")
     ap.add_argument("--no-tune", action="store_true",
                     help="library-default GEMM solutions (default: the measured per-shape table in "
                          "tread_amd/tuning, applied through PyTorch TunableOp)")
@@ -256,8 +265,11 @@ def main():
         per_token = 2 * cfg.num_hidden_layers * cfg.num_key_value_heads * cfg.head_dim * 2
         budget = per_token * (n_sys + tier_docs * doc_len)
         log(f"[bench] GPU tier: prefix + {tier_docs} of {n_docs} doc blocks ({budget / 1e6:.0f} MB); "
-            "the rest live in pinned host memory")
-    store = BlockStore(budget, 1 << 40)
+            f"the rest live {'on disk' if args.disk_tier else 'in pinned host memory'}")
+    if args.disk_tier:
+        store = BlockStore(budget, 0, disk_dir=args.disk_tier, disk_budget_bytes=1 << 40)
+    else:
+        store = BlockStore(budget, 1 << 40)
     eng = Engine(model, store, graphs=not args.eager)
     n_cold = COLD_DOCS.get(args.workload, 0)
     cold_gen = torch.Generator().manual_seed(3)
@@ -278,7 +290,7 @@ def main():
             log(f"[bench] warmup {i}: ttft {st.t['ttft'] * 1e3:.1f} ms hits {st.hits} misses {st.misses}")
         torch.cuda.synchronize()
         ttfts, stages = [], []
-        c0 = store.stats.cpu_hits
+        c0 = store.stats.cpu_hits + store.stats.disk_hits
         reqs = [request_docs() for _ in range(args.steps)]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -290,10 +302,11 @@ def main():
         wall = (time.perf_counter() - t0) / args.steps
         assert st.hits == 1 + n_docs - n_cold and st.misses == n_cold
         order = reqs[-1]
-        host_hits = (store.stats.cpu_hits - c0) / args.steps
+        host_hits = (store.stats.cpu_hits + store.stats.disk_hits - c0) / args.steps
         if host_hits:
-            log(f"[bench] host-tier hits per request: {host_hits:.1f} of {1 + n_docs} blocks "
-                "(promoted by H2D; evictions reuse the pinned copies)")
+            log(f"[bench] {'disk' if args.disk_tier else 'host'}-tier hits per request: {host_hits:.1f} of "
+                f"{1 + n_docs} blocks (promoted by H2D; evictions reuse the pinned copies"
+                f"{', files are written once' if args.disk_tier else ''})")
         log(f"[bench] timed: median ttft {statistics.median(ttfts) * 1e3:.1f} ms, wall/step {wall * 1e3:.1f} ms")
         if eng.last_selected is not None:
             S = eng.last_selected.double()
@@ -334,7 +347,8 @@ def main():
                    "doc_len": doc_len, "system": n_sys, "query": n_query, "recompute_ratio": args.ratio,
                    "policy": "deviation", "hipgraph": not args.eager, "gemm_tuning": not args.no_tune,
                    "gpu_tier_docs": n_docs if tier_docs is None else tier_docs, "cold_docs": n_cold,
-                   "host_tier_hits_per_request": host_hits, "parallelism": "single GPU"},
+                   "host_tier_hits_per_request": host_hits, "disk_tier": bool(args.disk_tier),
+                   "parallelism": "single GPU"},
         "stages_ms": med,
         "ttft_full_prefill_ms": None if full_ms is None else round(full_ms, 2),
         "speedup_vs_full_prefill": None if full_ms is None else round(full_ms / ttft_ms, 2),

@@ -444,3 +444,28 @@ def test_graph_decode_equals_eager_decode_and_generate_stops_like_the_reference(
     assert (toks, reason) == (ta[:j], "stop")
     toks, reason, _, _ = eager.generate(on(prefix), on(docs), on(query), max_tokens=0, ratio=0.3, policy="boundary")
     assert (toks, reason) == ([], "length")
+
+
+def test_disk_tier_gives_identical_results_and_survives_restart(setup, tmp_path):
+    """Blocks that left a two-block GPU tier for the disk tier (no host tier) and come back from
+    their files give bit-identical logits to GPU-tier hits; after persist(), a new engine and store
+    on the same directory (a restart) serve the whole request from disk, with identical logits."""
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=15)
+    big = Engine(gpu, BlockStore(1 << 30))
+    big.prefill(on(prefix), on(docs), on(query))
+    want, _, _ = big.prefill(on(prefix), on(docs[::-1]), on(query), ratio=0.3, policy="boundary")
+    nb = max(b.nbytes for b in big.store.blocks.values())
+    st = BlockStore(2 * nb, 0, disk_dir=tmp_path, disk_budget_bytes=1 << 30)
+    eng = Engine(gpu, st)
+    eng.prefill(on(prefix), on(docs), on(query))
+    got, _, s1 = eng.prefill(on(prefix), on(docs[::-1]), on(query), ratio=0.3, policy="boundary")
+    assert (s1.hits, s1.misses) == (1 + len(docs), 0) and st.stats.disk_hits > 0 and st.stats.spills > 0
+    assert torch.equal(got, want)
+    st.persist()
+    assert len(st.disk_blocks) == 1 + len(docs)
+    st2 = BlockStore(1 << 30, 0, disk_dir=tmp_path, disk_budget_bytes=1 << 30)
+    eng2 = Engine(gpu, st2)
+    again, _, s2 = eng2.prefill(on(prefix), on(docs[::-1]), on(query), ratio=0.3, policy="boundary")
+    assert (s2.hits, s2.misses, st2.stats.disk_hits) == (1 + len(docs), 0, 1 + len(docs))
+    assert torch.equal(again, want)

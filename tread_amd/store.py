@@ -19,17 +19,31 @@ at (`base`). What differs is how bytes move between tiers:
     per request and never back down.
 A block evicted and promoted again before its D2H was queued forces the pending copies out first,
 so an H2D never reads a host buffer before its D2H filled it.
-The store is single-threaded (callers serialise requests), as in the reference.
+
+With `disk_dir`, a third tier keeps blocks as files in the format of `tread_amd.blockfile` under a
+byte budget (LRU): a block leaving the host tier (or leaving the GPU tier when it does not fit the
+host tier) is written there by a background thread once its D2H has landed, unless its file
+already exists; blocks are immutable and content-addressed, so the disk tier is inclusive (a file
+stays after its block is promoted) and a file is written once. A lookup that misses the GPU and
+host tiers reads the file straight into pinned buffers (inside `batch()`, reads of several blocks
+run in parallel and the H2D schedule waits for them) and promotes the block like a host-tier hit.
+A new store on the same directory indexes the files found there, so cached blocks survive restarts.
+The store is single-threaded (callers serialise requests), as in the reference; only file I/O runs
+on helper threads.
 """
 import hashlib
+import os
 from collections import OrderedDict
+from concurrent.futures import ThreadPoolExecutor
 from contextlib import contextmanager
 from dataclasses import dataclass, field
+from pathlib import Path
 from typing import Optional
 
 import torch
 
 from tread_amd import _hip
+from tread_amd import blockfile
 
 
 def block_key(*parts) -> str:
@@ -100,17 +114,44 @@ class StoreStats:
     bytes_used: int = 0  # GPU tier
     cpu_hits: int = 0
     offloads: int = 0
-    cpu_evictions: int = 0  # blocks dropped for good from the host tier
+    cpu_evictions: int = 0  # blocks leaving the host tier (dropped, or kept by the disk tier)
     cpu_bytes_used: int = 0
+    disk_hits: int = 0  # lookups served from the disk tier (also counted in hits)
+    spills: int = 0  # block files written
+    disk_evictions: int = 0  # block files deleted for the disk budget
+    disk_bytes_used: int = 0
+
+
+class _DiskEntry:
+    """A block file of the disk tier: its header, and until its write is done the host block the
+    writer thread is reading (a lookup then serves that block instead of the file)."""
+
+    def __init__(self, header, path, block=None, job=None):
+        self.header, self.path, self.block, self.job = header, path, block, job
+
+    def settle(self):
+        if self.job is not None and self.job.done():
+            self.job.result()  # a failed write raises here
+            self.job, self.block = None, None
 
 
 class BlockStore:
-    def __init__(self, budget_bytes: int, cpu_budget_bytes: int = 0):
+    def __init__(self, budget_bytes: int, cpu_budget_bytes: int = 0, disk_dir=None, disk_budget_bytes: int = 0):
         self.budget = budget_bytes
         self.cpu_budget = cpu_budget_bytes
         self.blocks: "OrderedDict[str, Block]" = OrderedDict()  # GPU tier
         self.cpu_blocks: "OrderedDict[str, Block]" = OrderedDict()
         self.stats = StoreStats()
+        self.disk_dir = Path(disk_dir) if disk_dir is not None else None
+        self.disk_budget = disk_budget_bytes if disk_dir is not None else 0
+        self.disk_blocks: "OrderedDict[str, _DiskEntry]" = OrderedDict()
+        self._writer = self._readers = None
+        self._reads = []  # (future, Block) of disk reads the pending H2D schedule waits for
+        self._device = torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() \
+            else torch.device("cpu")
+        if self.disk_dir is not None:
+            self.disk_dir.mkdir(parents=True, exist_ok=True)
+            self._scan_disk()
         self._streams = {}  # "h2d" / "d2h" -> torch.cuda.Stream (default priority)
         # (event, tensors) of DMAs in flight: pinned buffers stay referenced until their copy ends,
         # since the DMA is not visible to torch's pinned-memory allocator.
@@ -149,6 +190,10 @@ class BlockStore:
     def flush(self):
         """Queue the pending DMAs: promotions layer-major on the H2D stream, then evictions on the
         D2H stream."""
+        if self._reads:
+            reads, self._reads = self._reads, []
+            for fut, _ in reads:
+                fut.result()  # the file's bytes are in the pinned buffers (or its error raises)
         if self._h2d:
             pend, self._h2d = self._h2d, []
             dev = pend[0][0].K.device
@@ -234,11 +279,15 @@ class BlockStore:
             self.blocks.move_to_end(key)
         else:
             b = self.cpu_blocks.pop(key, None)
-            if b is None:
-                self.stats.misses += 1
-                return None
-            self.stats.cpu_bytes_used -= b.nbytes
-            self.stats.cpu_hits += 1
+            if b is not None:
+                self.stats.cpu_bytes_used -= b.nbytes
+                self.stats.cpu_hits += 1
+            else:
+                b = self._from_disk(key)
+                if b is None:
+                    self.stats.misses += 1
+                    return None
+                self.stats.disk_hits += 1
             self._to_device(b)
             self._insert(key, b)
         b.hits += 1
@@ -253,6 +302,9 @@ class BlockStore:
         for tier in (self.blocks, self.cpu_blocks):
             if key in tier:
                 self._remove(tier, key)
+        if key in self.disk_blocks:
+            self._drop_file(key)
+        self._device = K.device
         b = Block(K=K, V=V, base=base, n_tokens=K.shape[-2], nbytes=nbytes, device=K.device)
         self._insert(key, b)
         return b
@@ -268,16 +320,127 @@ class BlockStore:
         self.stats.bytes_used -= b.nbytes
         self.stats.evictions += 1
         if b.nbytes > self.cpu_budget:
+            if self._disk_wants(key, b):  # no room in the host tier: straight to disk
+                self._spill(key, self._to_host(b))
             return
         while self.stats.cpu_bytes_used + b.nbytes > self.cpu_budget:
-            _, old = self.cpu_blocks.popitem(last=False)
+            okey, old = self.cpu_blocks.popitem(last=False)
             self.stats.cpu_bytes_used -= old.nbytes
             self.stats.cpu_evictions += 1
+            if self._disk_wants(okey, old):
+                self._spill(okey, old)
         # A new Block, never the evicted object: a request holding the old one keeps GPU tensors.
         nb = self._to_host(b)
         self.cpu_blocks[key] = nb
         self.stats.cpu_bytes_used += nb.nbytes
         self.stats.offloads += 1
+
+    # ---- disk tier
+    def _scan_disk(self):
+        """Index the block files already in disk_dir, oldest first (partial writes are removed)."""
+        for tmp in self.disk_dir.glob("*" + blockfile.SUFFIX + ".tmp"):
+            tmp.unlink(missing_ok=True)
+        files = sorted(self.disk_dir.glob("*" + blockfile.SUFFIX), key=lambda p: p.stat().st_mtime)
+        for path in files:
+            try:
+                h = blockfile.read_header(path)
+            except (OSError, blockfile.BlockFileError):
+                path.unlink(missing_ok=True)  # not a block of this format: not ours to serve
+                continue
+            if path.name != h["key"] + blockfile.SUFFIX:
+                continue
+            self._make_room(h["file_bytes"])
+            self.disk_blocks[h["key"]] = _DiskEntry(h, path)
+            self.stats.disk_bytes_used += h["file_bytes"]
+
+    def _disk_wants(self, key, b):
+        if self.disk_dir is None:
+            return False
+        if key in self.disk_blocks:  # written before: blocks never change
+            self.disk_blocks.move_to_end(key)
+            return False
+        return b.nbytes + blockfile.HEADER + blockfile.ALIGN <= self.disk_budget
+
+    def _make_room(self, nbytes):
+        while self.disk_blocks and self.stats.disk_bytes_used + nbytes > self.disk_budget:
+            self._drop_file(next(iter(self.disk_blocks)))
+            self.stats.disk_evictions += 1
+
+    def _drop_file(self, key):
+        e = self.disk_blocks.pop(key)
+        if e.job is not None:
+            e.job.result()
+        e.path.unlink(missing_ok=True)
+        self.stats.disk_bytes_used -= e.header["file_bytes"]
+
+    def _spill(self, key, hb):
+        """Write host block hb to the disk tier on the writer thread (after its D2H lands)."""
+        K, V = hb.K, hb.V
+        kb = K.numel() * K.element_size()
+        size = blockfile.HEADER + blockfile._align(kb) + kb  # the file: header, K padded to 4 KiB, V
+        self._make_room(size)
+        path = self.disk_dir / (key + blockfile.SUFFIX)
+        header = dict(key=key, base=hb.base, n_tokens=hb.n_tokens, shape=tuple(K.shape), dtype=K.dtype,
+                      file_bytes=size)
+        if self._writer is None:
+            self._writer = ThreadPoolExecutor(1, thread_name_prefix="tread-spill")
+        self._flush_if_pending(hb)
+
+        def job():
+            hb.synchronize()  # the D2H that fills the pinned buffers has landed
+            blockfile.write_block(path, key, K, V, hb.base)
+
+        self.disk_blocks[key] = _DiskEntry(header, path, block=hb, job=self._writer.submit(job))
+        self.stats.disk_bytes_used += size
+        self.stats.spills += 1
+
+    def _flush_if_pending(self, hb):
+        if hb.host_ready is _Pending:
+            self.flush()  # queue its D2H so that the writer can wait for it
+
+    def _from_disk(self, key):
+        e = self.disk_blocks.get(key)
+        if e is None:
+            return None
+        self.disk_blocks.move_to_end(key)
+        e.settle()
+        h = e.header
+        nbytes = 2 * int(torch.Size(h["shape"]).numel()) * torch.empty((), dtype=h["dtype"]).element_size()
+        if e.block is not None:  # still being written: serve the host copy the writer reads
+            src = e.block
+            return Block(K=src.K, V=src.V, base=src.base, n_tokens=src.n_tokens, nbytes=src.nbytes,
+                         device=self._device, host_ready=src.host_ready)
+        pin = self._device.type == "cuda"
+        K = torch.empty(h["shape"], dtype=h["dtype"], pin_memory=pin)
+        V = torch.empty(h["shape"], dtype=h["dtype"], pin_memory=pin)
+        b = Block(K=K, V=V, base=h["base"], n_tokens=h["n_tokens"], nbytes=nbytes, device=self._device)
+        if self._batch > 0 and pin:
+            if self._readers is None:
+                self._readers = ThreadPoolExecutor(min(8, os.cpu_count() or 1), thread_name_prefix="tread-read")
+            self._reads.append((self._readers.submit(blockfile.read_into, e.path, K, V, None), b))
+        else:
+            blockfile.read_into(e.path, K, V)
+        return b
+
+    def persist(self):
+        """Give every block of the GPU and host tiers that has no file yet one (within the disk
+        budget), and wait for all writes: after this a store on the same directory, in this or a
+        later process, finds the whole cache."""
+        if self.disk_dir is None:
+            return
+        for key, b in list(self.cpu_blocks.items()) + list(self.blocks.items()):
+            if self._disk_wants(key, b):
+                self._spill(key, self._to_host(b) if b.K.is_cuda else b)
+        self.flush()
+        self.drain()
+
+    def drain(self):
+        """Wait for every block file write (e.g. before the process exits or the directory is read
+        by another store)."""
+        for e in list(self.disk_blocks.values()):
+            if e.job is not None:
+                e.job.result()
+            e.settle()
 
     def _remove(self, tier, key):
         b = tier.pop(key)
@@ -287,4 +450,4 @@ class BlockStore:
             self.stats.cpu_bytes_used -= b.nbytes
 
     def __len__(self):
-        return len(self.blocks) + len(self.cpu_blocks)
+        return len(self.blocks) + len(self.cpu_blocks)  # the disk tier is inclusive, not counted
