@@ -239,8 +239,8 @@ def main():
                     help="benchmark GEMM solutions for every shape met (warm-up absorbs it) and write them here")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}); "
-              "the sharding design is described in DESIGN.md", file=sys.stderr)
+        print(f"bench.py measures one GPU: there is no multi-GPU path (asked for {args.gpus}); "
+              "the KV-head sharding is designed but not built", file=sys.stderr)
         sys.exit(2)
 
     from tread_amd import BlockStore, Engine, prefill_full

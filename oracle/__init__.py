@@ -9,7 +9,7 @@ This package restates, on the CPU with plain PyTorch ops, what the reference com
                       tread/graphs.py, op for op, including the bf16 rounding points.
 
 Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may import it, and
-only as the checker (or, for `cpu_baseline`, as the timed CPU path). The product package
+only to check results (or, for `cpu_baseline`, as the timed CPU path). The product package
 `tread_amd` never imports it and has no CPU fallback.
 
 How each function is pinned (checks live in tests/test_oracle_*.py):
