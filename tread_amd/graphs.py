@@ -37,9 +37,10 @@ def _q_room(n_query):
 
 
 def _q_bucket(n_query):
-    """Query rows of a captured query forward: a power of two >= 8 up to 256, then multiples of 256."""
+    """Query rows of a captured query forward: a power of two up to 256 (one row for a decode
+    step: padded rows cost attention work), then multiples of 256."""
     if n_query <= 256:
-        return max(8, 1 << (n_query - 1).bit_length())
+        return 1 << (n_query - 1).bit_length()
     return -(-n_query // 256) * 256
 
 
