@@ -23,7 +23,7 @@ typedef void* tread_event_t;  /* hipEvent_t */
 
 /* Thread-local text of the last error (empty string if none). */
 const char* tread_last_error(void);
-/* ABI version of this header (4); bumps on any signature change. */
+/* ABI version of this header (6); bumps on any signature change. */
 int tread_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------
@@ -128,10 +128,29 @@ int tread_silu_mul_bf16(const void* gate_up, int64_t n, int inter, void* out, tr
  * multiple of 128; x rows ldx apart (16-byte aligned), y rows ldy apart; bias may be NULL.
  * Replaces the q|k|v, o, gate|up, down and lm_head projections (transformers Qwen2Attention /
  * Qwen2MLP / lm_head) of the decoding step model(nxt.view(1, 1), past_key_values=cache) at
- * tread/server.py:207, whose GEMMs are weight-streaming.
+ * tread/server.py:207, whose GEMMs are weight-streaming. Layers with few output features split k
+ * across work groups when ws holds tread_skinny_workspace_bytes(m, n, k) bytes (device, 16-byte
+ * aligned); with ws NULL or too small the call still succeeds, unsplit.
  */
+size_t tread_skinny_workspace_bytes(int64_t m, int64_t n, int64_t k);
 int tread_skinny_linear_bf16(const void* x, int64_t ldx, const void* weight, const void* bias, int64_t m, int64_t n,
-                             int64_t k, void* y, int64_t ldy, tread_stream_t stream);
+                             int64_t k, void* y, int64_t ldy, void* ws, size_t ws_bytes, tread_stream_t stream);
+
+/* The same for m <= 8 rows with the layer's input norm fused in front: y = linear(RMSNorm(h + delta))
+ * (add_rmsnorm's bits), and h_out = h + delta (may be NULL; delta may be NULL). h, delta, h_out:
+ * [m, k] contiguous. Replaces input_layernorm / post_attention_layernorm + q|k|v or gate|up of a
+ * decoding step (transformers Qwen2DecoderLayer under tread/server.py:207).
+ */
+int tread_skinny_norm_linear_bf16(const void* h, const void* delta, const void* ln_weight, float eps, int64_t m,
+                                  int64_t n, int64_t k, const void* weight, const void* bias, void* y, void* h_out,
+                                  tread_stream_t stream);
+
+/* y[m, n] = linear(bf16(bf16(silu(g)) * u)) for gate_up [m, 2 inter] = [g | u], m <= 8 (silu_mul's
+ * bits fused into the down projection of a decoding step, transformers Qwen2MLP). ws as for
+ * tread_skinny_linear_bf16 with k = inter.
+ */
+int tread_skinny_silu_linear_bf16(const void* gate_up, int64_t m, int64_t inter, const void* weight, int64_t n, void* y,
+                                  void* ws, size_t ws_bytes, tread_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------
  * (d) Block-tier copy: async DMA of `bytes` between pinned host and device memory (either

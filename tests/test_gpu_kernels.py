@@ -175,7 +175,8 @@ def test_silu_mul_vs_torch():
 
 @pytest.mark.parametrize("m,n,k,bias,ldx", [(1, 32, 256, False, 256), (8, 4608, 3584, True, 3584),
                                              (3, 96, 512, True, 640), (32, 3584, 4608, False, 4608),
-                                             (17, 1024, 4096, False, 4096)])
+                                             (17, 1024, 4096, False, 4096), (8, 3584, 18944, False, 18944),
+                                             (1, 37888, 3584, False, 3584), (5, 32, 16384, True, 16384)])
 def test_skinny_linear_matches_fp32_reference(m, n, k, bias, ldx):
     """y = x W^T (+ b) of a few rows against the fp32 product of the same bf16 values: within one
     bf16 ulp of it plus the fp32 reordering error (1e-5 of the sum of |terms|, which matters only
@@ -193,6 +194,40 @@ def test_skinny_linear_matches_fp32_reference(m, n, k, bias, ldx):
     ulp = 2.0 ** (ref.abs().clamp_min(1e-30).log2().floor() - 7)
     assert ((got.float() - ref).abs() <= ulp + 1e-5 * terms).all()
     assert (bf16_ulps(got, ref.to(torch.bfloat16)) == 0).float().mean().item() > 0.95
+
+
+def test_skinny_linear_splits_k_for_few_features():
+    """Few output features split K over work groups (fp32 partials + a reduce kernel); many do not."""
+    assert _hip.lib().tread_skinny_workspace_bytes(8, 3584, 18944) == 4 * 8 * 3584 * 4
+    assert _hip.lib().tread_skinny_workspace_bytes(1, 37888, 3584) == 0  # many features
+    assert _hip.lib().tread_skinny_workspace_bytes(8, 3584, 3584) == 0  # short K
+    assert _hip.lib().tread_skinny_workspace_bytes(5, 32, 16384) == 4 * 5 * 32 * 4
+
+
+@pytest.mark.parametrize("m,H,n,with_delta,bias", [(1, 3584, 4608, True, True), (8, 512, 1536, True, False),
+                                                     (3, 256, 96, False, False)])
+def test_skinny_norm_linear_equals_norm_then_linear(m, H, n, with_delta, bias):
+    """The fused norm prologue gives add_rmsnorm's bits: its output equals skinny_linear applied
+    to add_rmsnorm's output bit for bit, and h_out equals add_rmsnorm's sum."""
+    g = torch.Generator().manual_seed(m + H)
+    h = torch.randn(m, H, generator=g).to(torch.bfloat16).to(DEV)
+    d = torch.randn(m, H, generator=g).to(torch.bfloat16).to(DEV) if with_delta else None
+    lnw = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(DEV)
+    W = (0.05 * torch.randn(n, H, generator=g)).to(torch.bfloat16).to(DEV)
+    b = torch.randn(n, generator=g).to(torch.bfloat16).to(DEV) if bias else None
+    y, hs = _hip.skinny_norm_linear(h, d, lnw, 1e-6, W, b)
+    s, x = _hip.add_rmsnorm(h, lnw, 1e-6, delta=d)
+    assert torch.equal(hs, s)
+    assert torch.equal(y, _hip.skinny_linear(x, W, b))
+
+
+@pytest.mark.parametrize("m,inter,n", [(1, 18944, 3584), (8, 512, 256), (2, 4096, 64)])
+def test_skinny_silu_linear_equals_silu_mul_then_linear(m, inter, n):
+    g = torch.Generator().manual_seed(m + inter)
+    gu = torch.randn(m, 2 * inter, generator=g).to(torch.bfloat16).to(DEV)
+    W = (0.05 * torch.randn(n, inter, generator=g)).to(torch.bfloat16).to(DEV)
+    y = _hip.skinny_silu_linear(gu, W)
+    assert torch.equal(y, _hip.skinny_linear(_hip.silu_mul(gu), W))
 
 
 def test_skinny_linear_rejects_unsupported_shapes():

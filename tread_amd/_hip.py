@@ -10,7 +10,7 @@ from pathlib import Path
 import torch  # loads torch's HIP runtime first, so the library below binds to the same one
 
 LIB_PATH = Path(__file__).resolve().with_name("libtread_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 6
 
 c_i64, c_int, c_void, c_float, c_size = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
 P_I64 = ctypes.POINTER(ctypes.c_int64)
@@ -39,7 +39,12 @@ _SIGS = {
                                        c_i64, c_float, c_void, c_void, c_size, c_void]),
     "tread_add_rmsnorm_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_int, c_void, c_void, c_void]),
     "tread_silu_mul_bf16": (c_int, [c_void, c_i64, c_int, c_void, c_void]),
-    "tread_skinny_linear_bf16": (c_int, [c_void, c_i64, c_void, c_void, c_i64, c_i64, c_i64, c_void, c_i64, c_void]),
+    "tread_skinny_workspace_bytes": (c_size, [c_i64, c_i64, c_i64]),
+    "tread_skinny_linear_bf16": (c_int, [c_void, c_i64, c_void, c_void, c_i64, c_i64, c_i64, c_void, c_i64, c_void,
+                                         c_size, c_void]),
+    "tread_skinny_norm_linear_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_i64, c_i64, c_void, c_void,
+                                              c_void, c_void, c_void]),
+    "tread_skinny_silu_linear_bf16": (c_int, [c_void, c_i64, c_i64, c_void, c_i64, c_void, c_void, c_size, c_void]),
     "tread_copy_async": (c_int, [c_void, c_void, c_size, c_void, c_void]),
     "tread_copy_layers_async": (c_int, [c_void, c_void, c_void, c_int, c_int, c_void, c_void]),
 }
@@ -210,9 +215,58 @@ def skinny_linear(x, weight, bias=None, out=None):
         raise ValueError(f"skinny_linear: unsupported shape x {tuple(x.shape)} weight {tuple(weight.shape)}")
     if out is None:
         out = torch.empty(m, n, dtype=x.dtype, device=x.device)
+    wsb = lib().tread_skinny_workspace_bytes(m, n, k)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=x.device) if wsb else None
     _check("tread_skinny_linear_bf16", lib().tread_skinny_linear_bf16(
-        _ptr(x), x.stride(0), _ptr(weight), _ptr(bias), m, n, k, _ptr(out), out.stride(0), _stream()))
+        _ptr(x), x.stride(0), _ptr(weight), _ptr(bias), m, n, k, _ptr(out), out.stride(0), _ptr(ws), wsb, _stream()))
     return out
+
+
+FUSED_MAX_ROWS = 8
+
+
+def fused_ok(m, n, k):
+    """Shapes of the fused-prologue skinny kernels (rows <= 8)."""
+    return 0 < m <= FUSED_MAX_ROWS and skinny_ok(m, n, k)
+
+
+def skinny_norm_linear(h, delta, ln_w, eps, weight, bias=None):
+    """(linear(RMSNorm(h + delta)), h + delta) for a few rows h [m, k]: the layer-input norm fused in
+    front of the projection. delta may be None (then the second result is h itself)."""
+    _need(h, "h")
+    _need(weight, "weight")
+    _need(ln_w, "ln_w")
+    if delta is not None:
+        _need(delta, "delta")
+    if bias is not None:
+        _need(bias, "bias")
+    m, k = h.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k or not fused_ok(m, n, k) or (delta is not None and delta.shape != h.shape):
+        raise ValueError(f"skinny_norm_linear: unsupported shape h {tuple(h.shape)} weight {tuple(weight.shape)}")
+    y = torch.empty(m, n, dtype=h.dtype, device=h.device)
+    h_out = torch.empty_like(h) if delta is not None else None
+    _check("tread_skinny_norm_linear_bf16", lib().tread_skinny_norm_linear_bf16(
+        _ptr(h), _ptr(delta), _ptr(ln_w), float(eps), m, n, k, _ptr(weight), _ptr(bias), _ptr(y), _ptr(h_out),
+        _stream()))
+    return y, (h_out if h_out is not None else h)
+
+
+def skinny_silu_linear(gate_up, weight):
+    """linear(silu(g) * u) for a few rows gate_up [m, 2 inter] = [g | u]: SiLU-gating fused into
+    the down projection."""
+    _need(gate_up, "gate_up")
+    _need(weight, "weight")
+    m, two_i = gate_up.shape
+    inter, n = two_i // 2, weight.shape[0]
+    if weight.shape[1] != inter or not fused_ok(m, n, inter):
+        raise ValueError(f"skinny_silu_linear: unsupported shape {tuple(gate_up.shape)} x {tuple(weight.shape)}")
+    y = torch.empty(m, n, dtype=gate_up.dtype, device=gate_up.device)
+    wsb = lib().tread_skinny_workspace_bytes(m, n, inter)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gate_up.device) if wsb else None
+    _check("tread_skinny_silu_linear_bf16", lib().tread_skinny_silu_linear_bf16(
+        _ptr(gate_up), m, inter, _ptr(weight), n, _ptr(y), _ptr(ws), wsb, _stream()))
+    return y
 
 
 def silu_mul(gate_up, out=None):

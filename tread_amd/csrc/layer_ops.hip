@@ -92,57 +92,8 @@ __global__ void add_rmsnorm_kernel(const bf16_t* __restrict__ x, const bf16_t* _
                                    bf16_t* __restrict__ norm_out) {
   __shared__ float red[32];
   const int64_t i = blockIdx.x;
-  const int nch = hidden / 8;
-  const bf16_t* xr = x + i * hidden;
-  u32x4_t v[CPT];
-  float ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < CPT; ++j) {
-    int c = threadIdx.x + j * blockDim.x;
-    if (c < nch) {
-      u32x4_t a = *reinterpret_cast<const u32x4_t*>(xr + c * 8);
-      if (delta) {
-        u32x4_t d = *reinterpret_cast<const u32x4_t*>(delta + i * hidden + c * 8);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) a[q] = pack_bf(lo_bf(a[q]) + lo_bf(d[q]), hi_bf(a[q]) + hi_bf(d[q]));
-        if (sum_out) *reinterpret_cast<u32x4_t*>(sum_out + i * hidden + c * 8) = a;
-      }
-      v[j] = a;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float l = lo_bf(a[q]), h = hi_bf(a[q]);
-        ss = fmaf(l, l, ss);
-        ss = fmaf(h, h, ss);
-      }
-    }
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-  const int wid = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-  if ((threadIdx.x & 63) == 0) red[wid] = ss;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float t = 0.f;
-    for (int k = 0; k < nw; ++k) t += red[k];
-    red[31] = 1.0f / sqrtf(t / (float)hidden + eps);
-  }
-  __syncthreads();
-  const float r = red[31];
-#pragma unroll
-  for (int j = 0; j < CPT; ++j) {
-    int c = threadIdx.x + j * blockDim.x;
-    if (c < nch) {
-      u32x4_t ww = *reinterpret_cast<const u32x4_t*>(w + c * 8);
-      u32x4_t o;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float l = bf2f(f2bf(lo_bf(v[j][q]) * r)) * lo_bf(ww[q]);
-        float h = bf2f(f2bf(hi_bf(v[j][q]) * r)) * hi_bf(ww[q]);
-        o[q] = pack_bf(l, h);
-      }
-      *reinterpret_cast<u32x4_t*>(norm_out + i * hidden + c * 8) = o;
-    }
-  }
+  add_rmsnorm_row<CPT>(x + i * hidden, delta ? delta + i * hidden : nullptr, w, eps, hidden, blockDim.x,
+                       sum_out && delta ? sum_out + i * hidden : nullptr, norm_out + i * hidden, red);
 }
 
 __global__ void silu_mul_kernel(const bf16_t* __restrict__ gu, int64_t n, int inter, bf16_t* __restrict__ out) {
@@ -156,8 +107,8 @@ __global__ void silu_mul_kernel(const bf16_t* __restrict__ gu, int64_t n, int in
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       float gl = lo_bf(g[q]), gh = hi_bf(g[q]);
-      float sl = bf2f(f2bf(gl / (1.0f + expf(-gl))));
-      float sh = bf2f(f2bf(gh / (1.0f + expf(-gh))));
+      float sl = silu_bf16(gl);
+      float sh = silu_bf16(gh);
       o[q] = pack_bf(sl * lo_bf(u[q]), sh * hi_bf(u[q]));
     }
     *reinterpret_cast<u32x4_t*>(out + i * inter + c) = o;
@@ -216,7 +167,7 @@ extern "C" int tread_add_rmsnorm_bf16(const void* x, const void* delta, const vo
     return fail(TREAD_EINVAL, "add_rmsnorm: hidden %d must be a multiple of 8 and <= 16384", hidden);
   if (n > 0x7fffffffLL) return fail(TREAD_ERANGE, "add_rmsnorm: n too large");
   int nch = hidden / 8;
-  int threads = nch >= 256 ? 256 : ((nch + 63) / 64) * 64;
+  int threads = rmsnorm_threads(hidden);
   int cpt = (nch + threads - 1) / threads;
   dim3 g((unsigned)n), b(threads);
   hipStream_t s = (hipStream_t)stream;

@@ -7,6 +7,9 @@
 // (l / 32) * 8 -- one 16-byte load), B = the token rows as columns (lane l: token l % 32, the same
 // 8 K; tokens >= M load nothing and stay zero). The 8 partial 32 x 32 tiles meet in LDS, and one
 // thread per (token, feature) sums them, adds the bias and rounds once to bf16 (as F.linear does).
+// A layer with few output features (fewer than 448 such work groups) and a long K also splits K
+// across 2, 4 or 8 work groups per tile: their fp32 sums meet in a workspace, and a second small
+// kernel adds them and the bias and rounds once.
 #include "common.h"
 #include "../../include/tread_hip.h"
 
@@ -16,39 +19,93 @@ constexpr int SK_WAVES = 8;
 constexpr int SK_ROWS = 32;  // output features per work group
 constexpr int SK_U = 4;      // K steps (16 each) whose loads are issued together
 
-__global__ __launch_bounds__(SK_WAVES * 64) void skinny_gemm_kernel(const bf16_t* __restrict__ x, int64_t ldx,
-                                                                   const bf16_t* __restrict__ w,
-                                                                   const bf16_t* __restrict__ bias,
-                                                                   bf16_t* __restrict__ y, int64_t ldy, int M, int K) {
+enum { PRO_NONE = 0, PRO_NORM = 1, PRO_SILU = 2 };
+
+struct SkinnyArgs {
+  const bf16_t* x;  // PRO_NONE: the rows; PRO_NORM: residual rows h; PRO_SILU: gate|up rows
+  int64_t ldx;
+  const bf16_t* delta;  // PRO_NORM: added to h (may be null), rows ldx apart
+  const bf16_t* lnw;    // PRO_NORM: RMSNorm weight
+  float eps;
+  bf16_t* h_out;        // PRO_NORM: h + delta, [M, K] contiguous (may be null)
+  int64_t inter;        // PRO_SILU: u of column k sits at column inter + k
+  const bf16_t* w;
+  const bf16_t* bias;
+  bf16_t* y;
+  int64_t ldy;
+  float* part;
+  int M, K, N;
+};
+
+// blockIdx.y = q selects the K slice [q K / ks, (q + 1) K / ks); with ks > 1 the slice's fp32 sums
+// go to part[q][m][n] and skinny_reduce_kernel finishes them.
+// PRO_NORM stages norm(h + delta) of the M rows in LDS first (add_rmsnorm_row: the same bits as
+// the stand-alone add + RMSNorm kernel) and work group (0, 0) writes h + delta to h_out; PRO_SILU
+// stages this work group's K slice of bf16(bf16(silu(g)) * u) (the same bits as silu_mul_kernel).
+template <int PRO, int CPT>
+__global__ __launch_bounds__(SK_WAVES * 64) void skinny_gemm_kernel(const SkinnyArgs a) {
+  extern __shared__ __align__(16) bf16_t xs[];  // staged operand rows (PRO_NORM / PRO_SILU)
   __shared__ float red[SK_WAVES][16][64];
+  __shared__ float nred[32];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int r32 = lane & 31, half = lane >> 5;
+  const int M = a.M, K = a.K;
   const int64_t n0 = (int64_t)blockIdx.x * SK_ROWS;
-  const int kw = K / SK_WAVES;  // a multiple of 16
-  const int kb = wv * kw + half * 8;
-  const bf16_t* wp = w + (n0 + r32) * (int64_t)K + kb;
+  const int ks = gridDim.y, q = blockIdx.y;
+  const int kslice = K / ks, k0 = q * kslice;
+  const int kw = kslice / SK_WAVES;  // a multiple of 16
+  const int kb = k0 + wv * kw + half * 8;  // this lane's first K
+  const bf16_t* wp = a.w + (n0 + r32) * (int64_t)K + kb;
   const bool xon = r32 < M;
-  const bf16_t* xp = x + (int64_t)(xon ? r32 : 0) * ldx + kb;
+  const int xrow = xon ? r32 : 0;
   const u32x4_t zero = {0u, 0u, 0u, 0u};
   f32x16_t acc = {};
   const int steps = kw / 16;
-  int s = 0;
-  for (; s + SK_U <= steps; s += SK_U) {
-    u32x4_t a[SK_U], b[SK_U];
+
+  auto mainloop = [&](const bf16_t* xp) {
+    int s = 0;
+    for (; s + SK_U <= steps; s += SK_U) {
+      u32x4_t av[SK_U], bv[SK_U];
 #pragma unroll
-    for (int u = 0; u < SK_U; ++u) a[u] = *reinterpret_cast<const u32x4_t*>(wp + (s + u) * 16);
+      for (int u = 0; u < SK_U; ++u) av[u] = *reinterpret_cast<const u32x4_t*>(wp + (s + u) * 16);
 #pragma unroll
-    for (int u = 0; u < SK_U; ++u) b[u] = xon ? *reinterpret_cast<const u32x4_t*>(xp + (s + u) * 16) : zero;
+      for (int u = 0; u < SK_U; ++u) bv[u] = xon ? *reinterpret_cast<const u32x4_t*>(xp + (s + u) * 16) : zero;
 #pragma unroll
-    for (int u = 0; u < SK_U; ++u)
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a[u]), __builtin_bit_cast(bf16x8_t, b[u]),
+      for (int u = 0; u < SK_U; ++u)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, av[u]),
+                                                      __builtin_bit_cast(bf16x8_t, bv[u]), acc, 0, 0, 0);
+    }
+    for (; s < steps; ++s) {
+      const u32x4_t av = *reinterpret_cast<const u32x4_t*>(wp + s * 16);
+      const u32x4_t bv = xon ? *reinterpret_cast<const u32x4_t*>(xp + s * 16) : zero;
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
                                                     acc, 0, 0, 0);
-  }
-  for (; s < steps; ++s) {
-    const u32x4_t a = *reinterpret_cast<const u32x4_t*>(wp + s * 16);
-    const u32x4_t b = xon ? *reinterpret_cast<const u32x4_t*>(xp + s * 16) : zero;
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), acc,
-                                                  0, 0, 0);
+    }
+  };
+
+  if constexpr (PRO == PRO_NONE) {
+    mainloop(a.x + (int64_t)xrow * a.ldx + kb);
+  } else if constexpr (PRO == PRO_NORM) {  // K is the hidden size, ks == 1
+    const int nthr = rmsnorm_threads(K);
+    const bool writer = a.h_out && blockIdx.x == 0 && blockIdx.y == 0;
+    for (int m = 0; m < M; ++m)
+      add_rmsnorm_row<CPT>(a.x + m * a.ldx, a.delta ? a.delta + m * a.ldx : nullptr, a.lnw, a.eps, K, nthr,
+                           writer ? a.h_out + (int64_t)m * K : nullptr, xs + m * K, nred);
+    mainloop(xs + xrow * K + (kb - k0));
+  } else {
+    const int cpr = kslice / 8;  // 16-byte chunks per staged row
+    for (int c = threadIdx.x; c < M * cpr; c += SK_WAVES * 64) {
+      const int m = c / cpr, kk = (c % cpr) * 8;
+      const bf16_t* gr = a.x + m * a.ldx + k0 + kk;
+      const u32x4_t g = *reinterpret_cast<const u32x4_t*>(gr);
+      const u32x4_t u = *reinterpret_cast<const u32x4_t*>(gr + a.inter);
+      u32x4_t o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = pack_bf(silu_bf16(lo_bf(g[j])) * lo_bf(u[j]), silu_bf16(hi_bf(g[j])) * hi_bf(u[j]));
+      *reinterpret_cast<u32x4_t*>(xs + m * kslice + kk) = o;
+    }
+    __syncthreads();
+    mainloop(xs + xrow * kslice + (kb - k0));
   }
 #pragma unroll
   for (int r = 0; r < 16; ++r) red[wv][r][lane] = acc[r];
@@ -59,29 +116,150 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_gemm_kernel(const bf16_t
     const int r = (row >> 3) * 4 + (row & 3), ln = m + 32 * ((row >> 2) & 1);
     float v = 0.f;
 #pragma unroll
-    for (int q = 0; q < SK_WAVES; ++q) v += red[q][r][ln];
-    if (bias) v += bf2f(bias[n0 + row]);
-    y[(int64_t)m * ldy + n0 + row] = f2bf(v);
+    for (int p = 0; p < SK_WAVES; ++p) v += red[p][r][ln];
+    if (ks > 1) {
+      a.part[((int64_t)q * M + m) * a.N + n0 + row] = v;
+    } else {
+      if (a.bias) v += bf2f(a.bias[n0 + row]);
+      a.y[(int64_t)m * a.ldy + n0 + row] = f2bf(v);
+    }
   }
+}
+
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ part, int ks, int M, int N,
+                                                            const bf16_t* __restrict__ bias, bf16_t* __restrict__ y,
+                                                            int64_t ldy) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)M * N) return;
+  const int m = (int)(t / N), n = (int)(t % N);
+  float v = 0.f;
+  for (int q = 0; q < ks; ++q) v += part[((int64_t)q * M + m) * N + n];
+  if (bias) v += bf2f(bias[n]);
+  y[(int64_t)m * ldy + n] = f2bf(v);
+}
+
+// K slices per 32-feature tile: enough work groups to cover the GPU when the feature count is small,
+// as long as every wave keeps at least 32 steps of 16 (shorter slices measured slower than one
+// work group per tile) and K splits into whole steps.
+static int skinny_ksplit(int64_t m, int64_t n, int64_t k) {
+  const int64_t tiles = n / SK_ROWS;
+  int ks = 1;
+  while (ks < 8 && tiles * ks < 448 && (k % ((int64_t)SK_WAVES * 16 * ks * 2)) == 0 &&
+         k / ((int64_t)SK_WAVES * 16 * ks * 2) >= 32)
+    ks *= 2;
+  (void)m;
+  return ks;
 }
 
 }  // namespace tread
 
 using namespace tread;
 
-extern "C" int tread_skinny_linear_bf16(const void* x, int64_t ldx, const void* weight, const void* bias, int64_t m,
-                                        int64_t n, int64_t k, void* y, int64_t ldy, tread_stream_t stream) {
-  if (m == 0 || n == 0) return 0;
-  if (m < 0 || m > 32 || n < 0 || k <= 0) return fail(TREAD_EINVAL, "skinny_linear: bad shape (m=%lld n=%lld k=%lld)",
-                                                      (long long)m, (long long)n, (long long)k);
-  if (!x || !weight || !y) return fail(TREAD_EINVAL, "skinny_linear: null pointer");
+static int launch_skinny(int pro, int cpt, const SkinnyArgs& a, int ks, size_t lds, hipStream_t s) {
+  const dim3 grid((unsigned)(a.N / SK_ROWS), (unsigned)ks), block(SK_WAVES * 64);
+  if (pro == PRO_NONE) hipLaunchKernelGGL((skinny_gemm_kernel<PRO_NONE, 1>), grid, block, lds, s, a);
+  else if (pro == PRO_SILU) hipLaunchKernelGGL((skinny_gemm_kernel<PRO_SILU, 1>), grid, block, lds, s, a);
+  else if (cpt <= 1) hipLaunchKernelGGL((skinny_gemm_kernel<PRO_NORM, 1>), grid, block, lds, s, a);
+  else if (cpt <= 2) hipLaunchKernelGGL((skinny_gemm_kernel<PRO_NORM, 2>), grid, block, lds, s, a);
+  else if (cpt <= 4) hipLaunchKernelGGL((skinny_gemm_kernel<PRO_NORM, 4>), grid, block, lds, s, a);
+  else hipLaunchKernelGGL((skinny_gemm_kernel<PRO_NORM, 8>), grid, block, lds, s, a);
+  int rc = check_launch("skinny_linear");
+  if (rc || ks <= 1) return rc;
+  const int64_t total = (int64_t)a.M * a.N;
+  hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, (const float*)a.part,
+                     ks, a.M, a.N, a.bias, a.y, a.ldy);
+  return check_launch("skinny_linear");
+}
+
+static int check_shape(const char* what, int64_t m, int64_t mmax, int64_t n, int64_t k) {
+  if (m < 0 || m > mmax || n < 0 || k <= 0)
+    return fail(TREAD_EINVAL, "%s: bad shape (m=%lld n=%lld k=%lld)", what, (long long)m, (long long)n, (long long)k);
   if ((n % SK_ROWS) != 0 || (k % (SK_WAVES * 16)) != 0)
-    return fail(TREAD_EINVAL, "skinny_linear: n=%lld must be a multiple of %d and k=%lld of %d", (long long)n, SK_ROWS,
+    return fail(TREAD_EINVAL, "%s: n=%lld must be a multiple of %d and k=%lld of %d", what, (long long)n, SK_ROWS,
                 (long long)k, SK_WAVES * 16);
+  if (n / SK_ROWS > 0x7fffffffLL || k > 0x7fffffffLL) return fail(TREAD_ERANGE, "%s: too large", what);
+  return 0;
+}
+
+extern "C" size_t tread_skinny_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || m > 32 || n <= 0 || (n % SK_ROWS) != 0 || k <= 0 || (k % (SK_WAVES * 16)) != 0) return 0;
+  const int ks = skinny_ksplit(m, n, k);
+  return ks > 1 ? (size_t)ks * m * n * sizeof(float) : 0;
+}
+
+extern "C" int tread_skinny_linear_bf16(const void* x, int64_t ldx, const void* weight, const void* bias, int64_t m,
+                                        int64_t n, int64_t k, void* y, int64_t ldy, void* ws, size_t ws_bytes,
+                                        tread_stream_t stream) {
+  if (m == 0 || n == 0) return 0;
+  if (int rc = check_shape("skinny_linear", m, 32, n, k)) return rc;
+  if (!x || !weight || !y) return fail(TREAD_EINVAL, "skinny_linear: null pointer");
   if (ldx < k || ldy < n || (ldx % 8) != 0) return fail(TREAD_EINVAL, "skinny_linear: bad leading dimensions");
   if ((((uintptr_t)x | (uintptr_t)weight) & 15) != 0) return fail(TREAD_EINVAL, "skinny_linear: x/weight not 16-byte aligned");
-  if (n / SK_ROWS > 0x7fffffffLL || k > 0x7fffffffLL) return fail(TREAD_ERANGE, "skinny_linear: too large");
-  hipLaunchKernelGGL(skinny_gemm_kernel, dim3((unsigned)(n / SK_ROWS)), dim3(SK_WAVES * 64), 0, (hipStream_t)stream,
-                     (const bf16_t*)x, ldx, (const bf16_t*)weight, (const bf16_t*)bias, (bf16_t*)y, ldy, (int)m, (int)k);
-  return check_launch("skinny_linear");
+  int ks = skinny_ksplit(m, n, k);
+  if (ks > 1 && (!ws || ws_bytes < (size_t)ks * m * n * sizeof(float) || (((uintptr_t)ws) & 15) != 0)) ks = 1;
+  SkinnyArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = (const bf16_t*)x;
+  a.ldx = ldx;
+  a.w = (const bf16_t*)weight;
+  a.bias = (const bf16_t*)bias;
+  a.y = (bf16_t*)y;
+  a.ldy = ldy;
+  a.part = (float*)ws;
+  a.M = (int)m;
+  a.K = (int)k;
+  a.N = (int)n;
+  return launch_skinny(PRO_NONE, 1, a, ks, 0, (hipStream_t)stream);
+}
+
+extern "C" int tread_skinny_norm_linear_bf16(const void* h, const void* delta, const void* ln_weight, float eps,
+                                             int64_t m, int64_t n, int64_t k, const void* weight, const void* bias,
+                                             void* y, void* h_out, tread_stream_t stream) {
+  if (m == 0 || n == 0) return 0;
+  if (int rc = check_shape("skinny_norm_linear", m, 8, n, k)) return rc;
+  if (k > 16384) return fail(TREAD_EINVAL, "skinny_norm_linear: hidden %lld above 16384", (long long)k);
+  if (!h || !ln_weight || !weight || !y) return fail(TREAD_EINVAL, "skinny_norm_linear: null pointer");
+  if ((((uintptr_t)h | (uintptr_t)delta | (uintptr_t)ln_weight | (uintptr_t)weight | (uintptr_t)h_out) & 15) != 0)
+    return fail(TREAD_EINVAL, "skinny_norm_linear: operands not 16-byte aligned");
+  SkinnyArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = (const bf16_t*)h;
+  a.ldx = k;
+  a.delta = (const bf16_t*)delta;
+  a.lnw = (const bf16_t*)ln_weight;
+  a.eps = eps;
+  a.h_out = (bf16_t*)h_out;
+  a.w = (const bf16_t*)weight;
+  a.bias = (const bf16_t*)bias;
+  a.y = (bf16_t*)y;
+  a.ldy = n;
+  a.M = (int)m;
+  a.K = (int)k;
+  a.N = (int)n;
+  const int nthr = rmsnorm_threads((int)k), cpt = (int)((k / 8 + nthr - 1) / nthr);
+  return launch_skinny(PRO_NORM, cpt, a, 1, (size_t)m * k * sizeof(bf16_t), (hipStream_t)stream);
+}
+
+extern "C" int tread_skinny_silu_linear_bf16(const void* gate_up, int64_t m, int64_t inter, const void* weight,
+                                             int64_t n, void* y, void* ws, size_t ws_bytes, tread_stream_t stream) {
+  if (m == 0 || n == 0) return 0;
+  if (int rc = check_shape("skinny_silu_linear", m, 8, n, inter)) return rc;
+  if (!gate_up || !weight || !y) return fail(TREAD_EINVAL, "skinny_silu_linear: null pointer");
+  if ((((uintptr_t)gate_up | (uintptr_t)weight) & 15) != 0)
+    return fail(TREAD_EINVAL, "skinny_silu_linear: operands not 16-byte aligned");
+  int ks = skinny_ksplit(m, n, inter);
+  if (ks > 1 && (!ws || ws_bytes < (size_t)ks * m * n * sizeof(float) || (((uintptr_t)ws) & 15) != 0)) ks = 1;
+  SkinnyArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = (const bf16_t*)gate_up;
+  a.ldx = 2 * inter;
+  a.inter = inter;
+  a.w = (const bf16_t*)weight;
+  a.y = (bf16_t*)y;
+  a.ldy = n;
+  a.part = (float*)ws;
+  a.M = (int)m;
+  a.K = (int)inter;
+  a.N = (int)n;
+  return launch_skinny(PRO_SILU, 1, a, ks, (size_t)m * (inter / ks) * sizeof(bf16_t), (hipStream_t)stream);
 }

@@ -48,6 +48,8 @@ def layer_forward(P, l, h, delta, R: Rows, K, V, kv_only=False):
     Returns (h, delta) entering layer l+1, or (h, None) when kv_only (k/v spliced, nothing else)."""
     lw = P.layers[l]
     hq, hkv, hd = P.hq, P.hkv, P.hd
+    if not kv_only and _few_rows(P, lw, h.shape[0]):
+        return _layer_few_rows(P, l, lw, h, delta, R, K, V)
     h, x = _hip.add_rmsnorm(h, lw.ln1, P.eps, delta=delta)
     n = h.shape[0]
     if kv_only:
@@ -63,6 +65,25 @@ def layer_forward(P, l, h, delta, R: Rows, K, V, kv_only=False):
     h, x = _hip.add_rmsnorm(h, lw.ln2, P.eps, delta=a)
     m = _hip.silu_mul(F.linear(x, lw.wgu))
     return h, F.linear(m, lw.wd)
+
+
+def _few_rows(P, lw, n):
+    return (n <= _hip.FUSED_MAX_ROWS and _hip.fused_ok(n, lw.wqkv.shape[0], P.H)
+            and _hip.fused_ok(n, lw.wgu.shape[0], P.H) and _hip.fused_ok(n, lw.wd.shape[0], lw.wd.shape[1]))
+
+
+def _layer_few_rows(P, l, lw, h, delta, R, K, V):
+    """layer_forward for a few rows (a decoding step): weight-streaming skinny kernels with the two
+    norms fused in front of q|k|v and gate|up and the SiLU gating in front of down, so a layer is
+    q|k|v, RoPE + splice, attention, o, gate|up, down: same roundings as the unfused layer."""
+    hq, hkv, hd = P.hq, P.hkv, P.hd
+    qkv, h = _hip.skinny_norm_linear(h, delta, lw.ln1, P.eps, lw.wqkv, lw.bqkv)
+    q = torch.empty(h.shape[0], hq, hd, dtype=h.dtype, device=h.device)
+    _hip.qkv_rope_splice(qkv, R.cos, R.sin, R.rows, hq, hkv, hd, K[l], V[l], q_out=q)
+    o = _hip.subset_attn(q, K[l], V[l], R.kend, hq, hkv, hd, P.scale, kseg=R.kseg, n_shared=R.n_shared)
+    a = F.linear(o, lw.wo)
+    gu, h = _hip.skinny_norm_linear(h, a, lw.ln2, P.eps, lw.wgu)
+    return h, _hip.skinny_silu_linear(gu, lw.wd)
 
 
 def run_layers(P, h, delta, R, K, V, layers, kv_only_last=False, hook=None):
@@ -85,11 +106,17 @@ def lm_head(P, x):
     return F.linear(x, P.lm_head)
 
 
+def norm_logits(P, h, delta):
+    """Final RMSNorm + lm_head of the rows h (+ delta) [m, H]; one fused kernel for a few rows."""
+    if _hip.fused_ok(h.shape[0], P.lm_head.shape[0], P.lm_head.shape[1]):
+        return _hip.skinny_norm_linear(h, delta, P.norm, P.eps, P.lm_head)[0]
+    _, x = _hip.add_rmsnorm(h, P.norm, P.eps, delta=delta)
+    return lm_head(P, x)
+
+
 def final_logits(P, h, delta):
     """Final RMSNorm + lm_head on the last row only (num_logits_to_keep=1). Returns [vocab]."""
-    _, x = _hip.add_rmsnorm(h[-1:].contiguous(), P.norm, P.eps,
-                            delta=None if delta is None else delta[-1:].contiguous())
-    return lm_head(P, x)[0]
+    return norm_logits(P, h[-1:].contiguous(), None if delta is None else delta[-1:].contiguous())[0]
 
 
 def embed(P, ids):

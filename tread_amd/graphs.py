@@ -17,8 +17,7 @@ from collections import OrderedDict
 
 import torch
 
-from tread_amd import _hip
-from tread_amd.forward import alloc_cache, embed, lm_head, make_rows, run_layers
+from tread_amd.forward import alloc_cache, embed, make_rows, norm_logits, run_layers
 
 
 def _bucket(n, T, n_min=64, n_step=256, t_step=1024):
@@ -73,8 +72,7 @@ class _QueryGraph:
         def body():
             R = make_rows(P, self.pos)
             h, d = run_layers(P, embed(P, self.ids), None, R, g.Kl, g.Vl, range(P.L))
-            _, x = _hip.add_rmsnorm(h.index_select(0, self.last), P.norm, P.eps, delta=d.index_select(0, self.last))
-            return lm_head(P, x)[0]
+            return norm_logits(P, h.index_select(0, self.last), d.index_select(0, self.last))[0]
 
         self.graph, self.out = _capture(body, device)
 
