@@ -23,7 +23,7 @@ typedef void* tread_event_t;  /* hipEvent_t */
 
 /* Thread-local text of the last error (empty string if none). */
 const char* tread_last_error(void);
-/* ABI version of this header (6); bumps on any signature change. */
+/* ABI version of this header (7); bumps on any signature change. */
 int tread_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------
@@ -146,9 +146,12 @@ int tread_skinny_norm_linear_bf16(const void* h, const void* delta, const void* 
                                   tread_stream_t stream);
 
 /* y[m, n] = linear(bf16(bf16(silu(g)) * u)) for gate_up [m, 2 inter] = [g | u], m <= 8 (silu_mul's
- * bits fused into the down projection of a decoding step, transformers Qwen2MLP). ws as for
- * tread_skinny_linear_bf16 with k = inter.
+ * bits fused into the down projection of a decoding step, transformers Qwen2MLP). ws: at least
+ * tread_skinny_silu_workspace_bytes(m, n, inter) bytes (device, 16-byte aligned; required when
+ * that is non-zero: the k split also keeps the staged rows within LDS).
+ * skinny_norm_linear requires m * k * 2 bytes to fit in LDS (about 127 KiB).
  */
+size_t tread_skinny_silu_workspace_bytes(int64_t m, int64_t n, int64_t inter);
 int tread_skinny_silu_linear_bf16(const void* gate_up, int64_t m, int64_t inter, const void* weight, int64_t n, void* y,
                                   void* ws, size_t ws_bytes, tread_stream_t stream);
 

@@ -230,6 +230,31 @@ def test_skinny_silu_linear_equals_silu_mul_then_linear(m, inter, n):
     assert torch.equal(y, _hip.skinny_linear(_hip.silu_mul(gu), W))
 
 
+def test_fused_skinny_kernels_keep_their_staged_rows_in_lds():
+    """Rows that would overflow LDS: the norm-fused kernel refuses them (the layer then runs
+    unfused); the SiLU-fused kernel splits K further (here 8 rows of a 28 672-wide gate|up)."""
+    g = torch.Generator().manual_seed(3)
+    h = torch.randn(8, 8192, generator=g).to(torch.bfloat16).to(DEV)
+    lnw = torch.ones(8192, dtype=torch.bfloat16, device=DEV)
+    W = (0.02 * torch.randn(64, 8192, generator=g)).to(torch.bfloat16).to(DEV)
+    assert not _hip.norm_fused_ok(8, 64, 8192) and _hip.norm_fused_ok(7, 64, 8192)
+    with pytest.raises(ValueError):
+        _hip.skinny_norm_linear(h, None, lnw, 1e-5, W)
+    y, _ = _hip.skinny_norm_linear(h[:7].contiguous(), None, lnw, 1e-5, W)
+    _, x = _hip.add_rmsnorm(h[:7].contiguous(), lnw, 1e-5)
+    assert torch.equal(y, _hip.skinny_linear(x, W))
+    inter, n = 28672, 512
+    gu = torch.randn(8, 2 * inter, generator=g).to(torch.bfloat16).to(DEV)
+    Wd = (0.02 * torch.randn(n, inter, generator=g)).to(torch.bfloat16).to(DEV)
+    assert _hip.lib().tread_skinny_silu_workspace_bytes(8, n, inter) > 0
+    got = _hip.skinny_silu_linear(gu, Wd).float().cpu()
+    act = _hip.silu_mul(gu).float().cpu()
+    ref = act @ Wd.float().cpu().T
+    terms = act.abs() @ Wd.float().cpu().abs().T
+    ulp = 2.0 ** (ref.abs().clamp_min(1e-30).log2().floor() - 7)
+    assert bool(((got - ref).abs() <= ulp + 1e-5 * terms).all())
+
+
 def test_skinny_linear_rejects_unsupported_shapes():
     x = torch.zeros(33, 256, device=DEV, dtype=torch.bfloat16)
     with pytest.raises(ValueError):

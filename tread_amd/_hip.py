@@ -10,7 +10,7 @@ from pathlib import Path
 import torch  # loads torch's HIP runtime first, so the library below binds to the same one
 
 LIB_PATH = Path(__file__).resolve().with_name("libtread_hip.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 c_i64, c_int, c_void, c_float, c_size = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
 P_I64 = ctypes.POINTER(ctypes.c_int64)
@@ -44,6 +44,7 @@ _SIGS = {
                                          c_size, c_void]),
     "tread_skinny_norm_linear_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_i64, c_i64, c_void, c_void,
                                               c_void, c_void, c_void]),
+    "tread_skinny_silu_workspace_bytes": (c_size, [c_i64, c_i64, c_i64]),
     "tread_skinny_silu_linear_bf16": (c_int, [c_void, c_i64, c_i64, c_void, c_i64, c_void, c_void, c_size, c_void]),
     "tread_copy_async": (c_int, [c_void, c_void, c_size, c_void, c_void]),
     "tread_copy_layers_async": (c_int, [c_void, c_void, c_void, c_int, c_int, c_void, c_void]),
@@ -225,9 +226,17 @@ def skinny_linear(x, weight, bias=None, out=None):
 FUSED_MAX_ROWS = 8
 
 
+FUSED_STAGE_BYTES = 127 * 1024  # LDS the norm-fused kernel may stage its rows in
+
+
 def fused_ok(m, n, k):
     """Shapes of the fused-prologue skinny kernels (rows <= 8)."""
     return 0 < m <= FUSED_MAX_ROWS and skinny_ok(m, n, k)
+
+
+def norm_fused_ok(m, n, k):
+    """fused_ok, and the m normed rows of k fit in LDS."""
+    return fused_ok(m, n, k) and m * k * 2 <= FUSED_STAGE_BYTES
 
 
 def skinny_norm_linear(h, delta, ln_w, eps, weight, bias=None):
@@ -242,7 +251,7 @@ def skinny_norm_linear(h, delta, ln_w, eps, weight, bias=None):
         _need(bias, "bias")
     m, k = h.shape
     n = weight.shape[0]
-    if weight.shape[1] != k or not fused_ok(m, n, k) or (delta is not None and delta.shape != h.shape):
+    if weight.shape[1] != k or not norm_fused_ok(m, n, k) or (delta is not None and delta.shape != h.shape):
         raise ValueError(f"skinny_norm_linear: unsupported shape h {tuple(h.shape)} weight {tuple(weight.shape)}")
     y = torch.empty(m, n, dtype=h.dtype, device=h.device)
     h_out = torch.empty_like(h) if delta is not None else None
@@ -262,7 +271,7 @@ def skinny_silu_linear(gate_up, weight):
     if weight.shape[1] != inter or not fused_ok(m, n, inter):
         raise ValueError(f"skinny_silu_linear: unsupported shape {tuple(gate_up.shape)} x {tuple(weight.shape)}")
     y = torch.empty(m, n, dtype=gate_up.dtype, device=gate_up.device)
-    wsb = lib().tread_skinny_workspace_bytes(m, n, inter)
+    wsb = lib().tread_skinny_silu_workspace_bytes(m, n, inter)
     ws = torch.empty(wsb, dtype=torch.uint8, device=gate_up.device) if wsb else None
     _check("tread_skinny_silu_linear_bf16", lib().tread_skinny_silu_linear_bf16(
         _ptr(gate_up), m, inter, _ptr(weight), n, _ptr(y), _ptr(ws), wsb, _stream()))

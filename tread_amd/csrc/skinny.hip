@@ -171,6 +171,21 @@ static int launch_skinny(int pro, int cpt, const SkinnyArgs& a, int ks, size_t l
   return check_launch("skinny_linear");
 }
 
+// Dynamic LDS the staged operand rows may take: gfx950's 160 KiB per work group less the kernel's
+// static arrays (partial tiles 32 KiB, norm scratch) and some headroom.
+constexpr size_t SK_STAGE_MAX = 160 * 1024 - sizeof(float) * (SK_WAVES * 16 * 64 + 32) - 256;
+
+// K slices of the SiLU-gated projection: the plain rule, then more slices until this work group's
+// staged rows fit in LDS (0: no split fits).
+static int silu_ksplit(int64_t m, int64_t n, int64_t k) {
+  int ks = skinny_ksplit(m, n, k);
+  while ((size_t)m * (k / ks) * sizeof(bf16_t) > SK_STAGE_MAX) {
+    if (ks >= 64 || (k % ((int64_t)SK_WAVES * 16 * ks * 2)) != 0) return 0;
+    ks *= 2;
+  }
+  return ks;
+}
+
 static int check_shape(const char* what, int64_t m, int64_t mmax, int64_t n, int64_t k) {
   if (m < 0 || m > mmax || n < 0 || k <= 0)
     return fail(TREAD_EINVAL, "%s: bad shape (m=%lld n=%lld k=%lld)", what, (long long)m, (long long)n, (long long)k);
@@ -184,6 +199,12 @@ static int check_shape(const char* what, int64_t m, int64_t mmax, int64_t n, int
 extern "C" size_t tread_skinny_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || m > 32 || n <= 0 || (n % SK_ROWS) != 0 || k <= 0 || (k % (SK_WAVES * 16)) != 0) return 0;
   const int ks = skinny_ksplit(m, n, k);
+  return ks > 1 ? (size_t)ks * m * n * sizeof(float) : 0;
+}
+
+extern "C" size_t tread_skinny_silu_workspace_bytes(int64_t m, int64_t n, int64_t inter) {
+  if (m <= 0 || m > 8 || n <= 0 || (n % SK_ROWS) != 0 || inter <= 0 || (inter % (SK_WAVES * 16)) != 0) return 0;
+  const int ks = silu_ksplit(m, n, inter);
   return ks > 1 ? (size_t)ks * m * n * sizeof(float) : 0;
 }
 
@@ -218,6 +239,8 @@ extern "C" int tread_skinny_norm_linear_bf16(const void* h, const void* delta, c
   if (m == 0 || n == 0) return 0;
   if (int rc = check_shape("skinny_norm_linear", m, 8, n, k)) return rc;
   if (k > 16384) return fail(TREAD_EINVAL, "skinny_norm_linear: hidden %lld above 16384", (long long)k);
+  if ((size_t)m * k * sizeof(bf16_t) > SK_STAGE_MAX)
+    return fail(TREAD_EINVAL, "skinny_norm_linear: %lld rows of %lld do not fit in LDS", (long long)m, (long long)k);
   if (!h || !ln_weight || !weight || !y) return fail(TREAD_EINVAL, "skinny_norm_linear: null pointer");
   if ((((uintptr_t)h | (uintptr_t)delta | (uintptr_t)ln_weight | (uintptr_t)weight | (uintptr_t)h_out) & 15) != 0)
     return fail(TREAD_EINVAL, "skinny_norm_linear: operands not 16-byte aligned");
@@ -247,8 +270,11 @@ extern "C" int tread_skinny_silu_linear_bf16(const void* gate_up, int64_t m, int
   if (!gate_up || !weight || !y) return fail(TREAD_EINVAL, "skinny_silu_linear: null pointer");
   if ((((uintptr_t)gate_up | (uintptr_t)weight) & 15) != 0)
     return fail(TREAD_EINVAL, "skinny_silu_linear: operands not 16-byte aligned");
-  int ks = skinny_ksplit(m, n, inter);
-  if (ks > 1 && (!ws || ws_bytes < (size_t)ks * m * n * sizeof(float) || (((uintptr_t)ws) & 15) != 0)) ks = 1;
+  const int ks = silu_ksplit(m, n, inter);
+  if (ks == 0) return fail(TREAD_EINVAL, "skinny_silu_linear: %lld rows of %lld do not fit in LDS", (long long)m,
+                           (long long)inter);
+  if (ks > 1 && (!ws || ws_bytes < (size_t)ks * m * n * sizeof(float) || (((uintptr_t)ws) & 15) != 0))
+    return fail(TREAD_EINVAL, "skinny_silu_linear: needs a workspace of tread_skinny_silu_workspace_bytes() bytes");
   SkinnyArgs a;
   memset(&a, 0, sizeof(a));
   a.x = (const bf16_t*)gate_up;

@@ -68,8 +68,8 @@ def layer_forward(P, l, h, delta, R: Rows, K, V, kv_only=False):
 
 
 def _few_rows(P, lw, n):
-    return (n <= _hip.FUSED_MAX_ROWS and _hip.fused_ok(n, lw.wqkv.shape[0], P.H)
-            and _hip.fused_ok(n, lw.wgu.shape[0], P.H) and _hip.fused_ok(n, lw.wd.shape[0], lw.wd.shape[1]))
+    return (n <= _hip.FUSED_MAX_ROWS and _hip.norm_fused_ok(n, lw.wqkv.shape[0], P.H)
+            and _hip.norm_fused_ok(n, lw.wgu.shape[0], P.H) and _hip.fused_ok(n, lw.wd.shape[0], lw.wd.shape[1]))
 
 
 def _layer_few_rows(P, l, lw, h, delta, R, K, V):
@@ -108,7 +108,7 @@ def lm_head(P, x):
 
 def norm_logits(P, h, delta):
     """Final RMSNorm + lm_head of the rows h (+ delta) [m, H]; one fused kernel for a few rows."""
-    if _hip.fused_ok(h.shape[0], P.lm_head.shape[0], P.lm_head.shape[1]):
+    if _hip.norm_fused_ok(h.shape[0], P.lm_head.shape[0], P.lm_head.shape[1]):
         return _hip.skinny_norm_linear(h, delta, P.norm, P.eps, P.lm_head)[0]
     _, x = _hip.add_rmsnorm(h, P.norm, P.eps, delta=delta)
     return lm_head(P, x)
