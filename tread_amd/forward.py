@@ -67,23 +67,49 @@ def layer_forward(P, l, h, delta, R: Rows, K, V, kv_only=False):
     return h, F.linear(m, lw.wd)
 
 
+# A layer of at most FEW_ROWS rows (a decoding step, a short query) runs its projections on the
+# weight-streaming skinny kernels, which beat the library GEMM there on MI355X. The kernels with
+# the norm (or the SiLU gating) fused in front save a launch but redo that prologue in every work
+# group for every row; measured on MI355X they win up to NORM_FUSED_ROWS rows (norm) and
+# SILU_FUSED_ROWS rows (SiLU) and lose beyond (at 8 rows the norm-fused lm_head takes twice the
+# time of RMSNorm + skinny kernel). Fused or not, the results are the same bits.
+FEW_ROWS = 8
+NORM_FUSED_ROWS = 2
+SILU_FUSED_ROWS = 4
+
+
 def _few_rows(P, lw, n):
-    return (n <= _hip.FUSED_MAX_ROWS and _hip.norm_fused_ok(n, lw.wqkv.shape[0], P.H)
-            and _hip.norm_fused_ok(n, lw.wgu.shape[0], P.H) and _hip.fused_ok(n, lw.wd.shape[0], lw.wd.shape[1]))
+    return n <= FEW_ROWS and all(_hip.skinny_ok(n, w.shape[0], w.shape[1]) for w in (lw.wqkv, lw.wo, lw.wgu, lw.wd))
+
+
+def _norm_linear(P, h, delta, ln_w, weight, bias=None):
+    """(linear(RMSNorm(h + delta)), h + delta) for a few rows, on the skinny kernels."""
+    m = h.shape[0]
+    if m <= NORM_FUSED_ROWS and _hip.norm_fused_ok(m, weight.shape[0], weight.shape[1]):
+        return _hip.skinny_norm_linear(h, delta, ln_w, P.eps, weight, bias)
+    h, x = _hip.add_rmsnorm(h, ln_w, P.eps, delta=delta)
+    return _hip.skinny_linear(x, weight, bias), h
+
+
+def _silu_linear(gate_up, weight):
+    """linear(silu(g) * u) for a few rows, on the skinny kernels."""
+    m = gate_up.shape[0]
+    if m <= SILU_FUSED_ROWS and _hip.fused_ok(m, weight.shape[0], weight.shape[1]):
+        return _hip.skinny_silu_linear(gate_up, weight)
+    return _hip.skinny_linear(_hip.silu_mul(gate_up), weight)
 
 
 def _layer_few_rows(P, l, lw, h, delta, R, K, V):
-    """layer_forward for a few rows (a decoding step): weight-streaming skinny kernels with the two
-    norms fused in front of q|k|v and gate|up and the SiLU gating in front of down, so a layer is
-    q|k|v, RoPE + splice, attention, o, gate|up, down: same roundings as the unfused layer."""
+    """layer_forward for a few rows: (norm ->) q|k|v, RoPE + splice, attention, o, (norm ->)
+    gate|up, (SiLU ->) down, with the same roundings as the layer for many rows."""
     hq, hkv, hd = P.hq, P.hkv, P.hd
-    qkv, h = _hip.skinny_norm_linear(h, delta, lw.ln1, P.eps, lw.wqkv, lw.bqkv)
+    qkv, h = _norm_linear(P, h, delta, lw.ln1, lw.wqkv, lw.bqkv)
     q = torch.empty(h.shape[0], hq, hd, dtype=h.dtype, device=h.device)
     _hip.qkv_rope_splice(qkv, R.cos, R.sin, R.rows, hq, hkv, hd, K[l], V[l], q_out=q)
     o = _hip.subset_attn(q, K[l], V[l], R.kend, hq, hkv, hd, P.scale, kseg=R.kseg, n_shared=R.n_shared)
-    a = F.linear(o, lw.wo)
-    gu, h = _hip.skinny_norm_linear(h, a, lw.ln2, P.eps, lw.wgu)
-    return h, _hip.skinny_silu_linear(gu, lw.wd)
+    a = _hip.skinny_linear(o, lw.wo)
+    gu, h = _norm_linear(P, h, a, lw.ln2, lw.wgu)
+    return h, _silu_linear(gu, lw.wd)
 
 
 def run_layers(P, h, delta, R, K, V, layers, kv_only_last=False, hook=None):
@@ -101,14 +127,15 @@ def lm_head(P, x):
     """Logits of the rows x [m, H]. A few rows stream the vocab-sized weight through the skinny
     linear kernel (measured faster than the library GEMM at m <= 8 on MI355X); more rows use the
     library GEMM."""
-    if x.shape[0] <= 8 and _hip.skinny_ok(x.shape[0], P.lm_head.shape[0], P.lm_head.shape[1]):
+    if x.shape[0] <= FEW_ROWS and _hip.skinny_ok(x.shape[0], P.lm_head.shape[0], P.lm_head.shape[1]):
         return _hip.skinny_linear(x, P.lm_head)
     return F.linear(x, P.lm_head)
 
 
 def norm_logits(P, h, delta):
-    """Final RMSNorm + lm_head of the rows h (+ delta) [m, H]; one fused kernel for a few rows."""
-    if _hip.norm_fused_ok(h.shape[0], P.lm_head.shape[0], P.lm_head.shape[1]):
+    """Final RMSNorm + lm_head of the rows h (+ delta) [m, H]; one fused kernel for one or two rows."""
+    m = h.shape[0]
+    if m <= NORM_FUSED_ROWS and _hip.norm_fused_ok(m, P.lm_head.shape[0], P.lm_head.shape[1]):
         return _hip.skinny_norm_linear(h, delta, P.norm, P.eps, P.lm_head)[0]
     _, x = _hip.add_rmsnorm(h, P.norm, P.eps, delta=delta)
     return lm_head(P, x)
