@@ -107,9 +107,10 @@ class Engine:
         torch.cuda.current_stream().synchronize()
 
     @torch.inference_mode()
-    def prefix_block(self, prefix_ids, st, namespace=""):
-        """tread/engine.py:44-57."""
-        key = block_key(*self.sig, namespace, "prefix", prefix_ids)
+    def prefix_block(self, prefix_ids, st, namespace="", host_ids=None):
+        """tread/engine.py:44-57. `host_ids`: the same ids already in host memory (hashed instead of
+        prefix_ids, which saves a device-to-host copy per key)."""
+        key = block_key(*self.sig, namespace, "prefix", prefix_ids if host_ids is None else host_ids)
         b = self.store.get(key)
         if b is None:
             st.misses += 1
@@ -123,13 +124,14 @@ class Engine:
         return key, b
 
     @torch.inference_mode()
-    def doc_blocks(self, prefix_key, pb, docs, st):
+    def doc_blocks(self, prefix_key, pb, docs, st, host_docs=None):
         """tread/engine.py:59-96: look up every doc; prefill all misses in one packed forward.
 
         The packed sequence sits on top of the prefix rows of a temporary cache; token j of doc i
         has RoPE position P + j, writes cache row P + off_i + j, and sees rows [0, P) plus
-        [P + off_i, P + off_i + j]: the reference's block-diagonal mask, evaluated in-kernel."""
-        keys = [block_key(*self.sig, prefix_key, d) for d in docs]
+        [P + off_i, P + off_i + j]: the reference's block-diagonal mask, evaluated in-kernel.
+        `host_docs`: the docs' ids already in host memory, hashed instead of `docs`."""
+        keys = [block_key(*self.sig, prefix_key, d) for d in (docs if host_docs is None else host_docs)]
         blocks = [self.store.get(k) for k in keys]
         miss = [i for i, b in enumerate(blocks) if b is None]
         st.hits += len(docs) - len(miss)
@@ -167,9 +169,13 @@ class Engine:
         self._sync()
         t0 = time.perf_counter()
 
+        hp = hd = None
+        if prefix_ids.device.type != "cpu":  # one device-to-host copy for every key's ids
+            hp, *hd = torch.cat([prefix_ids] + list(docs)).to("cpu", torch.int64).split(
+                [len(prefix_ids)] + [len(d) for d in docs])
         with self.store.batch():  # host-tier hits share one layer-major H2D schedule
-            pkey, pb = self.prefix_block(prefix_ids, st, namespace)
-            blocks = self.doc_blocks(pkey, pb, docs, st)
+            pkey, pb = self.prefix_block(prefix_ids, st, namespace, host_ids=hp)
+            blocks = self.doc_blocks(pkey, pb, docs, st, host_docs=hd)
         Pn = pb.n_tokens
         T = Pn + sum(len(d) for d in docs)
         Nq = len(query_ids)
@@ -185,12 +191,11 @@ class Engine:
         else:
             K, V = alloc_cache(self.P, T + Nq + reserve, dev)
         sources = [(pb, 0, 0)]
-        cands = []
         offset = Pn
         for d, b in zip(docs, blocks):
             sources.append((b, offset, offset - b.base))
-            cands.append(torch.arange(offset, offset + len(d), device=d.device))
             offset += len(d)
+        cands = list(torch.arange(Pn, T, device=dev).split([len(d) for d in docs])) if docs else []
         asm = _Assembly(self.P, K, V, sources)
         Kl, Vl = K.unbind(0), V.unbind(0)
         self._sync()
