@@ -222,6 +222,8 @@ def main():
     ap.add_argument("--workload", default="qwen2.5-7b-32k", choices=list(WORKLOADS))
     ap.add_argument("--ratio", type=float, default=0.2)
     ap.add_argument("--eager", action="store_true", help="recompute loop without the hipGraph")
+    ap.add_argument("--no-fold", action="store_true",
+                    help="run the query forward after the recompute instead of inside it")
     ap.add_argument("--full-reps", type=int, default=3, help="full-prefill reps for the TTFT denominator (0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu", action="store_true")
@@ -270,7 +272,7 @@ def main():
         store = BlockStore(budget, 0, disk_dir=args.disk_tier, disk_budget_bytes=1 << 40)
     else:
         store = BlockStore(budget, 1 << 40)
-    eng = Engine(model, store, graphs=not args.eager)
+    eng = Engine(model, store, graphs=not args.eager, fold_query=not args.no_fold)
     n_cold = COLD_DOCS.get(args.workload, 0)
     cold_gen = torch.Generator().manual_seed(3)
 
@@ -345,7 +347,8 @@ def main():
         "data": "synthetic (uniform random token ids, random-init N(0,0.02) weights)",
         "config": {"workload": args.workload, "model": preset_name, "context_tokens": T, "docs": n_docs,
                    "doc_len": doc_len, "system": n_sys, "query": n_query, "recompute_ratio": args.ratio,
-                   "policy": "deviation", "hipgraph": not args.eager, "gemm_tuning": not args.no_tune,
+                   "policy": "deviation", "hipgraph": not args.eager, "query_folded": not args.no_fold,
+                   "gemm_tuning": not args.no_tune,
                    "gpu_tier_docs": n_docs if tier_docs is None else tier_docs, "cold_docs": n_cold,
                    "host_tier_hits_per_request": host_hits, "disk_tier": bool(args.disk_tier),
                    "parallelism": "single GPU"},

@@ -326,14 +326,16 @@ def test_eviction_respects_budget(setup):
     assert kl(full, out) < 1e-4
 
 
+@pytest.mark.parametrize("fold", [True, False])
 @pytest.mark.parametrize("policy,ratio", [("deviation", 0.2), ("boundary", 0.3), ("boundary", 1.0)])
-def test_graph_blend_matches_eager(setup, policy, ratio):
-    """tests/test_engine.py:95-113: the hipGraph replay equals the eager loop; one capture of the
-    recompute loop and one of the query forward, both replayed by the later requests."""
+def test_graph_blend_matches_eager(setup, policy, ratio, fold):
+    """tests/test_engine.py:95-113: the hipGraph replay equals the eager loop, and the captured
+    graphs are replayed by the later requests: one capture (the recompute loop, with the query
+    rows folded in, as the reference's count) or two (recompute loop, then the query forward)."""
     cfg, gpu, ref = setup
     prefix, docs, query = request(cfg, seed=11)
-    eager = Engine(gpu, BlockStore(1 << 30))
-    graphed = Engine(gpu, BlockStore(1 << 30), graphs=True)
+    eager = Engine(gpu, BlockStore(1 << 30), fold_query=fold)
+    graphed = Engine(gpu, BlockStore(1 << 30), graphs=True, fold_query=fold)
     eager.prefill(on(prefix), on(docs), on(query))
     graphed.prefill(on(prefix), on(docs), on(query))
     a, _, _ = eager.prefill(on(prefix), on(docs[::-1]), on(query), ratio=ratio, policy=policy)
@@ -341,10 +343,38 @@ def test_graph_blend_matches_eager(setup, policy, ratio):
         b, _, _ = graphed.prefill(on(prefix), on(docs[::-1]), on(query), ratio=ratio, policy=policy)
         assert kl(a, b) < 1e-4
         torch.cuda.synchronize()
-    assert graphed.runner.captures == 2
+    assert graphed.runner.captures == (1 if fold else 2)
     if ratio == 1.0:
         full, _, _ = prefill_full(gpu, on(prefix), on(docs[::-1]), on(query))
         assert kl(full, b) < 1e-4
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+@pytest.mark.parametrize("policy,ratio", [("deviation", 0.2), ("random", 0.5)])
+def test_folded_query_equals_query_after_the_recompute(setup, policy, ratio, graphs):
+    """The query rows riding in the recompute (blend_query) give the logits and the cache of the
+    reference's order (recompute every layer, then the query forward over the blended cache):
+    same selection, logits within the KL 1e-4 bar, and a cache (context and query rows) that
+    differs only by the bf16 roundings of GEMMs over a different row count (relative Frobenius
+    norm of the difference below 1 %)."""
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=15)
+    out = {}
+    for fold in (False, True):
+        eng = Engine(gpu, BlockStore(1 << 30), graphs=graphs, fold_query=fold)
+        eng.prefill(on(prefix), on(docs), on(query))
+        gen = torch.Generator().manual_seed(3)
+        logits, cache, st = eng.prefill(on(prefix), on(docs[::-1]), on(query), ratio=ratio, policy=policy, gen=gen)
+        n = cache.length
+        out[fold] = (logits.float(), cache.K[:, :, :, :n].float().clone(), cache.V[:, :, :, :n].float().clone(),
+                     eng.last_selected.clone(), st.recompute_eff)
+        torch.cuda.synchronize()
+    (la, Ka, Va, Sa, ea), (lb, Kb, Vb, Sb, eb) = out[False], out[True]
+    assert torch.equal(Sa, Sb) and ea == eb
+    assert kl(la, lb) < 1e-4
+    for A, B in ((Ka, Kb), (Va, Vb)):
+        rel = ((A - B).norm() / A.norm()).item()
+        assert rel < 1e-2, rel
 
 
 def test_empty_docs_and_zero_budget(setup):
@@ -436,7 +466,7 @@ def test_graph_decode_equals_eager_decode_and_generate_stops_like_the_reference(
     tb, sb, _ = _decode_steps(graphed, prefix, docs, query, 5, 0.3)
     for a, b in zip(sa, sb):
         assert kl(a, b) < 1e-5
-    assert graphed.runner.captures == 3  # recompute loop, query forward, one decode step
+    assert graphed.runner.captures == 2  # recompute loop (query rows folded in), one decode step
     toks, reason, st, cache = eager.generate(on(prefix), on(docs), on(query), max_tokens=5, ratio=0.3,
                                              policy="boundary")
     assert (toks, reason) == (ta, "length") and st.hits == 1 + len(docs)

@@ -161,15 +161,38 @@ def blend_cache(model, ctx_ids, K, V, candidates, ratio, policy, gen=None, runne
     `hook(l)`, if given, runs before layer l is first read (lazy assembly of in-flight blocks).
     With trim_last, the last layer only splices its k/v: its hidden output is discarded by the
     reference as well, so K/V are unchanged. Returns (S, eff)."""
+    S, eff, _ = _blend(model, ctx_ids, K, V, candidates, ratio, policy, gen, runner, graph, T, hook, trim_last, None)
+    return S, eff
+
+
+def blend_query(model, ctx_ids, K, V, candidates, ratio, policy, query_ids, T, gen=None, runner=None, graph=None,
+                hook=None, trim_last=True):
+    """blend_cache with the query forward of tread/engine.py:131-132 folded into the recompute: the
+    query rows (positions T, T+1, ...) join the recomputed rows from the first recomputed layer on
+    (with the deviation policy their layer 0 runs right after the deviation pass, on its own: 32
+    000 + 32 rows would cost the layer's GEMMs an extra row of tiles), so their projections ride
+    in the recompute's GEMMs.
+    Layer by layer they see what the reference's query forward sees afterwards: the layer's
+    recomputed rows are spliced before its attention, and a layer's cache does not change once
+    it is recomputed. At the last layer every row splices its k/v and only the query rows run the
+    rest. Returns (S, eff, logits of the last query row [vocab]); logits is None when nothing is
+    recomputed (the caller then runs the query forward itself). With `graph` the logits are the
+    graph's static output."""
+    return _blend(model, ctx_ids, K, V, candidates, ratio, policy, gen, runner, graph, T, hook, trim_last, query_ids)
+
+
+def _blend(model, ctx_ids, K, V, candidates, ratio, policy, gen, runner, graph, T, hook, trim_last, query_ids):
     P = prepared(model)
     dev = K[0].device
     if not candidates:
-        return torch.empty(0, dtype=torch.long, device=dev), 0.0
+        return torch.empty(0, dtype=torch.long, device=dev), 0.0, None
     all_c = torch.cat(candidates)
     n, budget = select(ratio, candidates)
     if budget == 0:
-        return all_c[:0], 0.0
-    start = 0
+        return all_c[:0], 0.0, None
+    nq = 0 if query_ids is None else query_ids.numel()
+    q_pos = torch.arange(T, T + nq, device=dev) if nq else None
+    start, hq = 0, None
     if policy == "boundary":
         rank = torch.cat([torch.arange(len(c), device=c.device) for c in candidates])
         S = all_c[rank.argsort(stable=True)[:budget]].sort().values
@@ -185,17 +208,30 @@ def blend_cache(model, ctx_ids, K, V, candidates, ratio, policy, gen=None, runne
         sel = _hip.topk_select(score, budget)  # ascending candidate indices => S sorted
         S = all_c[sel]
         h = h_all.index_select(0, sel)
+        if nq:  # the query rows' layer 0 (after every candidate's layer-0 k/v is in place)
+            hq, dq = layer_forward(P, 0, embed(P, query_ids), None, make_rows(P, q_pos), K, V)
+            hq = hq + dq  # the hidden entering layer 1, as the deviation pass returns it
         start = 1
     else:
         raise ValueError(policy)
+    if nq and hq is None:
+        hq = embed(P, query_ids)
+    logits = None
     if graph is not None:
-        runner.run(graph, h, S, T, hook=hook)
+        out = runner.run(graph, h, S, T, hook=hook, hq=hq)
+        logits = out if nq else None
+    elif nq:
+        R = make_rows(P, torch.cat([S, q_pos]))
+        keep = torch.arange(budget, budget + nq, device=dev) if trim_last else None
+        hk, dk = run_layers(P, torch.cat([h, hq]), None, R, K, V, range(start, P.L), kv_only_last=trim_last,
+                            hook=hook, keep=keep)
+        logits = final_logits(P, hk, dk)  # the query rows are last either way
     else:
         R = make_rows(P, S)
         run_layers(P, h, None, R, K, V, range(start, P.L), kv_only_last=trim_last, hook=hook)
     L = P.L
     eff = (len(S) * (L - start) + start * n) / (n * L)
-    return S, eff
+    return S, eff, logits
 
 
 def blend(model, ctx_ids, K, V, candidates, ratio, policy, gen=None, inplace=False, runner=None):

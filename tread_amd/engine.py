@@ -23,7 +23,7 @@ from dataclasses import dataclass, field
 import torch
 
 from tread_amd import _hip
-from tread_amd.blend import blend_cache, forward_into, prepared, select
+from tread_amd.blend import blend_cache, blend_query, forward_into, prepared, select
 from tread_amd.cache import KVCache
 from tread_amd.forward import alloc_cache, embed, final_logits, make_rows, run_layers
 from tread_amd.graphs import SubsetRunner
@@ -93,13 +93,16 @@ class _Assembly:
 
 
 class Engine:
-    def __init__(self, model, store: BlockStore, graphs=False):
+    def __init__(self, model, store: BlockStore, graphs=False, fold_query=True):
         self.model = model
         self.store = store
         self.P = prepared(model)
         # hipGraph replay of the recompute loop (tread/graphs.py); off by default as in the
         # reference, since each new size bucket pays a one-off capture.
         self.runner = SubsetRunner(model) if graphs else None
+        # with recompute, the query forward rides in the recompute loop (blend_query) instead of
+        # running after it: same per-layer inputs, one weight pass less
+        self.fold_query = fold_query
         self.sig = model_sig(model)
         self.last_selected = None  # positions recomputed by the last prefill (diagnostics)
 
@@ -185,7 +188,8 @@ class Engine:
             n, budget = select(ratio, docs)
             if budget > 0:
                 start = 1 if policy == "deviation" else 0
-                graph = self.runner.cache_for(start, budget, T, Nq, dev, room=Nq + reserve)
+                graph = self.runner.cache_for(start, budget, T, Nq, dev, room=Nq + reserve,
+                                              fold=self.fold_query and Nq > 0)
         if graph is not None:
             K, V = graph.K, graph.V
         else:
@@ -202,14 +206,23 @@ class Engine:
         t1 = time.perf_counter()
 
         self.last_selected = None
+        logits = None
         if ratio > 0:
             ctx = torch.cat([prefix_ids] + list(docs))
-            self.last_selected, st.recompute_eff = blend_cache(self.model, ctx, Kl, Vl, cands, ratio, policy, gen=gen,
-                                              runner=self.runner, graph=graph, T=T, hook=asm.ensure)
+            if self.fold_query and Nq > 0:  # the query rows ride in the recompute (blend_query)
+                self.last_selected, st.recompute_eff, logits = blend_query(
+                    self.model, ctx, Kl, Vl, cands, ratio, policy, query_ids, T, gen=gen, runner=self.runner,
+                    graph=graph, hook=asm.ensure)
+            else:
+                self.last_selected, st.recompute_eff = blend_cache(
+                    self.model, ctx, Kl, Vl, cands, ratio, policy, gen=gen, runner=self.runner, graph=graph, T=T,
+                    hook=asm.ensure)
         self._sync()
         t2 = time.perf_counter()
 
-        if graph is not None and Nq > 0:
+        if logits is not None:
+            logits = logits.clone()  # a graph's output is static
+        elif graph is not None and Nq > 0:
             logits = self.runner.query(graph, query_ids, T, hook=asm.ensure).clone()  # the graph's output is static
         else:
             R = make_rows(self.P, torch.arange(T, T + Nq, device=dev))

@@ -33,6 +33,12 @@ class Rows:
     def __len__(self):
         return self.rows.numel()
 
+    def select(self, idx):
+        """The rows at positions idx (int64 tensor) of this set."""
+        pick = lambda t: None if t is None else t.index_select(0, idx)
+        return Rows(rows=pick(self.rows), kend=pick(self.kend), cos=pick(self.cos), sin=pick(self.sin),
+                    kseg=pick(self.kseg), n_shared=self.n_shared)
+
 
 def make_rows(P, rows, pos=None, kseg=None, n_shared=0):
     """RoPE tables for `pos` (default: rows) and causal key ends = rows."""
@@ -112,14 +118,23 @@ def _layer_few_rows(P, l, lw, h, delta, R, K, V):
     return h, _silu_linear(gu, lw.wd)
 
 
-def run_layers(P, h, delta, R, K, V, layers, kv_only_last=False, hook=None):
+def run_layers(P, h, delta, R, K, V, layers, kv_only_last=False, hook=None, keep=None):
     """Run `layers` (an ordered range) for rows R; `hook(l)` runs before layer l (lazy assembly).
-    With kv_only_last, the last layer only splices its k/v (its hidden output is never used)."""
+    With kv_only_last, the last layer only splices its k/v (its hidden output is never used),
+    except for the rows at positions `keep` (int64 tensor), which then run it fully after every
+    row's k/v is in place; the result is those rows' (h, delta)."""
     layers = list(layers)
     for j, l in enumerate(layers):
         if hook is not None:
             hook(l)
-        h, delta = layer_forward(P, l, h, delta, R, K, V, kv_only=kv_only_last and j == len(layers) - 1)
+        last = kv_only_last and j == len(layers) - 1
+        if last and keep is not None:
+            hk = h.index_select(0, keep)
+            dk = None if delta is None else delta.index_select(0, keep)
+            layer_forward(P, l, h, delta, R, K, V, kv_only=True)
+            h, delta = layer_forward(P, l, hk, dk, R.select(keep), K, V)
+        else:
+            h, delta = layer_forward(P, l, h, delta, R, K, V, kv_only=last)
     return h, delta
 
 

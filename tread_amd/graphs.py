@@ -80,9 +80,14 @@ class _QueryGraph:
 class _Graph:
     """The recompute loop of one bucket, captured as one graph per group of `seg` layers that
     chain through static hidden-state tensors: a replay can then wait for each layer's host-tier
-    copies (and assemble them) right before that layer, instead of before the whole loop."""
+    copies (and assemble them) right before that layer, instead of before the whole loop.
 
-    def __init__(self, P, start, nb, Tb, t_cap, device, trim_last, seg=1):
+    Rows of a replay: the n recomputed positions, then (with nq > 0) nq query slots at T, T+1, ...
+    whose forward rides along (the last segment ends with the final norm + lm_head of query slot
+    `last`), then padding. Padded rows see no key (key end -1) and write their k/v to spare rows
+    no real row reads."""
+
+    def __init__(self, P, start, nb, Tb, t_cap, device, trim_last, seg=1, nq=0):
         self.t_cap = t_cap
         self.queries = {}  # nq -> _QueryGraph over this bucket's cache
         self.K, self.V = alloc_cache(P, t_cap, device)
@@ -91,6 +96,10 @@ class _Graph:
         self.Kl, self.Vl = self.K.unbind(0), self.V.unbind(0)
         self.h = torch.zeros(nb, P.H, dtype=P.embed.dtype, device=device)
         self.S = torch.arange(nb, dtype=torch.int64, device=device)
+        self.kend = self.S.clone()
+        self.nq = nq
+        self.q_idx = torch.arange(nb - nq, nb, dtype=torch.int64, device=device)
+        self.last = torch.zeros(1, dtype=torch.int64, device=device)
         self.nb, self.Tb, self.start = nb, Tb, start
         self.pool = torch.cuda.graph_pool_handle()
         layers = list(range(start, P.L))
@@ -103,11 +112,20 @@ class _Graph:
 
             def body(ls=ls, gi=gi, last=last):
                 if gi == 0:
-                    carry["R"] = make_rows(P, self.S)
+                    R = make_rows(P, self.S)
+                    R.kend = self.kend
+                    carry["R"] = R
                     h, delta = self.h, None
                 else:
                     h, delta = carry["out"][gi - 1]
-                return run_layers(P, h, delta, carry["R"], self.Kl, self.Vl, ls, kv_only_last=trim_last and last)
+                keep = self.q_idx if (nq and last and trim_last) else None
+                h, delta = run_layers(P, h, delta, carry["R"], self.Kl, self.Vl, ls,
+                                      kv_only_last=trim_last and last, keep=keep)
+                if not (nq and last):
+                    return h, delta
+                if keep is None:  # every row ran the last layer: pick the query slots
+                    h, delta = h.index_select(0, self.q_idx), delta.index_select(0, self.q_idx)
+                return norm_logits(P, h.index_select(0, self.last), delta.index_select(0, self.last))[0]
 
             carry.setdefault("out", [])
             graph, out = _capture(body, device, self.pool)
@@ -135,30 +153,34 @@ class SubsetRunner:
     def worth_it(self, T):
         return self.max_ctx is None or T <= self.max_ctx
 
-    def _graph(self, start, n, T, n_query, device):
-        nb, Tb = _bucket(n, T)
-        key = (start, nb, Tb, _q_room(n_query))
+    def _graph(self, start, n, T, n_query, device, nq=0):
+        nb, Tb = _bucket(n, T)  # the reference's bucket for the recomputed rows, plus the query slots
+        nb += nq
+        key = (start, nb, Tb, _q_room(n_query), nq)
         g = self.graphs.get(key)
         if g is None:
             while len(self.graphs) >= self.max_graphs:
                 self.graphs.popitem(last=False)
-            g = _Graph(self.P, start, nb, Tb, Tb + key[3], device, self.trim_last, self.seg)
+            g = _Graph(self.P, start, nb, Tb, Tb + key[3], device, self.trim_last, self.seg, nq)
             self.graphs[key] = g
             self.captures += 1
         self.graphs.move_to_end(key)
         return g
 
     @torch.inference_mode()
-    def cache_for(self, start, n, T, n_query, device, room=None):
+    def cache_for(self, start, n, T, n_query, device, room=None, fold=False):
         """The bucket graph serving a request that recomputes n rows from layer `start` over a
         T-row context followed by n_query query rows (and `room` >= n_query rows in all after the
-        context, for decoding); its .K/.V are the cache to assemble into. The query forward for
-        n_query rows is captured with it (before anything is assembled)."""
-        g = self._graph(start, n, T, max(n_query, room or 0), device)
-        nq = _q_bucket(n_query)
-        if n_query > 0 and nq not in g.queries:
-            g.queries[nq] = _QueryGraph(self.P, g, nq, device)
-            self.captures += 1
+        context, for decoding); its .K/.V are the cache to assemble into. With fold, the query rows
+        ride in the recompute graph (`run(..., hq=...)` returns the logits); otherwise the query
+        forward for n_query rows is captured beside it (before anything is assembled)."""
+        nq = _q_bucket(n_query) if (fold and n_query > 0) else 0
+        g = self._graph(start, n, T, max(n_query, room or 0), device, nq)
+        if n_query > 0 and not nq:
+            nqb = _q_bucket(n_query)
+            if nqb not in g.queries:
+                g.queries[nqb] = _QueryGraph(self.P, g, nqb, device)
+                self.captures += 1
         return g
 
     @torch.inference_mode()
@@ -197,18 +219,33 @@ class SubsetRunner:
         return self.query(g, ids, T)
 
     @torch.inference_mode()
-    def run(self, g, h, S, T, hook=None):
-        """Replay layers start..L-1 of bucket graph `g` for sorted positions S (len n <= g.nb) with
-        hidden rows h [n, H] over a T-row context. `hook(l)` runs before the graph segment holding
-        layer l (lazy assembly must complete before the replay reads that layer of the cache)."""
-        n = len(S)
-        if n > g.nb or T + g.nb - n > g.Tb:
-            raise ValueError(f"request (n={n}, T={T}) does not fit bucket (nb={g.nb}, Tb={g.Tb})")
+    def run(self, g, h, S, T, hook=None, hq=None):
+        """Replay layers start..L-1 of bucket graph `g` for sorted positions S (len n) with hidden
+        rows h [n, H] over a T-row context, and, for a bucket with query slots, the query rows hq
+        [m, H] (m <= g.nq) at positions T, T+1, ...; returns the last query row's logits then
+        (static), else the last segment's static (h, delta). `hook(l)` runs before the graph
+        segment holding layer l (lazy assembly must complete before the replay reads that layer)."""
+        n, m = len(S), (0 if hq is None else hq.shape[0])
+        rows = n + g.nq
+        pad = g.nb - rows
+        if rows > g.nb or T + pad > g.Tb or m > g.nq or (g.nq > 0) != (m > 0):
+            raise ValueError(f"request (n={n}, queries={m}, T={T}) does not fit bucket "
+                             f"(nb={g.nb}, Tb={g.Tb}, query slots={g.nq})")
+        dev = S.device
         g.S[:n].copy_(S)
         g.h[:n].copy_(h)
-        if n < g.nb:
-            g.S[n:].copy_(torch.arange(T, T + g.nb - n, device=S.device))
-            g.h[n:].zero_()
+        if g.nq:
+            g.S[n:rows].copy_(torch.arange(T, T + g.nq, device=dev))
+            g.h[n:n + m].copy_(hq)
+            g.q_idx.copy_(torch.arange(n, rows, device=dev))
+            g.last.fill_(m - 1)
+        if pad:
+            # padded rows: spare cache rows after the query slots, no visible key
+            g.S[rows:].copy_(torch.arange(T + g.nq, T + g.nq + pad, device=dev))
+        g.kend[:rows].copy_(g.S[:rows])
+        g.kend[rows:].fill_(-1)
+        if g.nb > n + m:
+            g.h[n + m:].zero_()
         for ls, graph in g.segs:
             if hook is not None:
                 for l in ls:

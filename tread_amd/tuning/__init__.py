@@ -3,7 +3,8 @@
 The decoder's GEMMs stay plain library GEMMs; TunableOp only chooses, per GEMM shape, which of the
 installed hipBLASLt / rocBLAS solutions runs. `gemm_gfx950_qwen2.5-7b.csv` holds the choices measured
 on MI355X for the 7B-shaped reuse workload (recompute rows at 20 % and 50 % of the doc tokens,
-deviation rows, query rows, full-prefill rows); TunableOp checks the file's torch / HIP / hipBLASLt / rocBLAS / arch stamps before using it.
+with and without the 32 query rows riding along, deviation rows, query rows, full-prefill rows);
+TunableOp checks the file's torch / HIP / hipBLASLt / rocBLAS / arch stamps before using it.
 Shapes missing from the table run the library default.
 """
 import os
