@@ -5,8 +5,10 @@ the graph's static buffers before each replay and back out after, which made gra
 2k tokens (tread/graphs.py:64-67,92-99). Here the static buffer of a bucket IS the assembled
 cache: the engine asks the runner for it before assembly (`cache_for`), the fused assemble kernel
 writes the request's blocks straight into it, and a replay only needs the selected positions S
-and their hidden rows copied in (a few MB). Padding follows the reference: padded query slots
-sit at positions T, T+1, ... inside the bucket's spare rows, which no real query can see.
+and their hidden rows copied in (a few MB). Padding follows the reference's buckets: padded
+rows sit in the bucket's spare rows after the context (and after the query slots when the query
+rows ride along), where no real row looks, and see no key themselves (key end -1), so they cost
+the GEMMs their rows but no attention.
 
 Each bucket holds one [L, 1, kv, t_cap, hd] K/V pair; the cache returned by the engine aliases
 it and stays valid until the next request replays the same bucket. The loop is captured as one

@@ -52,7 +52,7 @@ def block_key(*parts) -> str:
     h = hashlib.sha256()
     for p in parts:
         if isinstance(p, torch.Tensor):
-            h.update(p.detach().to("cpu", torch.int64).contiguous().numpy().tobytes())
+            h.update(p.detach().to("cpu", torch.int64).contiguous().numpy())  # its buffer, no copy
         else:
             h.update(str(p).encode())
         h.update(b"\x00")
