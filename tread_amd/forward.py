@@ -29,6 +29,7 @@ class Rows:
     sin: torch.Tensor
     kseg: Optional[torch.Tensor] = None  # int64 [n]: first row of token i's own segment
     n_shared: int = 0             # rows [0, n_shared) are visible to every token (with kseg)
+    gemm_split: int = 0           # > 0: the gate|up GEMM runs rows [0, split) and [split, n) apart
 
     def __len__(self):
         return self.rows.numel()
@@ -38,6 +39,18 @@ class Rows:
         pick = lambda t: None if t is None else t.index_select(0, idx)
         return Rows(rows=pick(self.rows), kend=pick(self.kend), cos=pick(self.cos), sin=pick(self.sin),
                     kseg=pick(self.kseg), n_shared=self.n_shared)
+
+
+def _gate_up(x, w, split):
+    """x @ w.T; with 0 < split < rows, as two GEMMs over rows [0, split) and [split, rows): when
+    a few rows ride on a row count that is a multiple of the library's 256-row tiles, the
+    vocabulary-wide gate|up GEMM then skips a whole extra row of tiles."""
+    if not 0 < split < x.shape[0]:
+        return F.linear(x, w)
+    y = torch.empty(x.shape[0], w.shape[0], dtype=x.dtype, device=x.device)
+    torch.mm(x[:split], w.t(), out=y[:split])
+    torch.mm(x[split:], w.t(), out=y[split:])
+    return y
 
 
 def make_rows(P, rows, pos=None, kseg=None, n_shared=0):
@@ -69,7 +82,7 @@ def layer_forward(P, l, h, delta, R: Rows, K, V, kv_only=False):
     o = _hip.subset_attn(q, K[l], V[l], R.kend, hq, hkv, hd, P.scale, kseg=R.kseg, n_shared=R.n_shared)
     a = F.linear(o, lw.wo)
     h, x = _hip.add_rmsnorm(h, lw.ln2, P.eps, delta=a)
-    m = _hip.silu_mul(F.linear(x, lw.wgu))
+    m = _hip.silu_mul(_gate_up(x, lw.wgu, R.gemm_split))
     return h, F.linear(m, lw.wd)
 
 

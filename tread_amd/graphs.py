@@ -116,6 +116,8 @@ class _Graph:
                 if gi == 0:
                     R = make_rows(P, self.S)
                     R.kend = self.kend
+                    if nq and (nb - nq) % 256 == 0:  # the query slots would add a row of GEMM tiles
+                        R.gemm_split = nb - nq
                     carry["R"] = R
                     h, delta = self.h, None
                 else:
