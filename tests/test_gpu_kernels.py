@@ -346,6 +346,11 @@ CASES = [
     (64, 8, 128, 1500, 90, "subset"),
     (8, 2, 128, 700, 337, "segments"),
     (14, 2, 64, 500, 230, "segments"),
+    # >= 8 row tiles per KV head and no key split: the longest quarter of the row tiles runs as
+    # two key-half work groups merged by attn_halves_kernel
+    (28, 4, 128, 1000, 1000, "subset"),
+    (28, 4, 128, 1000, 1000, "prefill"),
+    (14, 2, 64, 1000, 900, "segments"),
     # few rows over a long cache: split-K + combine
     (28, 4, 128, 20000, 32, "query"),
     (14, 2, 64, 9000, 5, "query"),

@@ -61,6 +61,7 @@ struct AttnArgs {
   int32_t xpg;    // XCDs per KV head (0: plain mapping)
   int32_t nsplit;
   int32_t split_len;  // keys per split (multiple of ATT_BK)
+  int32_t nlong;      // (nsplit 1) the nlong longest row tiles per KV head run as two work groups
   float scale_log2;
 };
 
@@ -207,6 +208,18 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     head = bid % a.hkv;
     td = bid / a.hkv;
   }
+  // Balance: the row tiles are ordered longest first (td 0 is the last row tile, whose rows see
+  // the most keys when rows are sorted by position), and the nlong longest run as two work groups
+  // over the two halves of their key tiles, dispatched first; the rest follow longest first.
+  int kpart = -1;
+  if (a.nsplit <= 1 && a.nlong > 0) {
+    if (td < 2 * a.nlong) {
+      kpart = td & 1;
+      td >>= 1;
+    } else {
+      td -= a.nlong;
+    }
+  }
   if (td >= a.tiles) return;
   const int tile = a.tiles - 1 - td;
 
@@ -261,7 +274,13 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   }
   const int nA = endA > startA ? (endA - startA + ATT_BK - 1) / ATT_BK : 0;
   const int nB = endB > startB ? (endB - startB + ATT_BK - 1) / ATT_BK : 0;
-  const int ntiles = nA + nB;
+  // this work group's key tiles [jbase, jbase + ntiles) of the nA + nB (a half for kpart 0 / 1)
+  int jbase = 0, ntiles = nA + nB;
+  if (kpart >= 0) {
+    const int h = ntiles / 2;
+    jbase = kpart ? h : 0;
+    ntiles = kpart ? ntiles - h : h;
+  }
 
   // ---- Q^T fragments (B operand), resident for the whole kernel, pre-multiplied by
   // scale * log2(e) (rounded to bf16, as the reference's math path rounds its scaled q), so that
@@ -296,7 +315,8 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     }
   }
 
-  auto tile_bounds = [&](int j, int& s0, int& s1) {
+  auto tile_bounds = [&](int jl, int& s0, int& s1) {
+    const int j = jbase + jl;
     if (j < nA) {
       s0 = startA + j * ATT_BK;
       s1 = min(s0 + ATT_BK, endA);
@@ -398,7 +418,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   auto settle = [&](int j, f32x16_t (&s)[2]) {
     int s0, s1;
     tile_bounds(j, s0, s1);
-    const bool full = (s1 - s0 == ATT_BK) && (s1 - 1 <= kmin) && (j < nA || s0 >= segmax);
+    const bool full = (s1 - s0 == ATT_BK) && (s1 - 1 <= kmin) && (jbase + j < nA || s0 >= segmax);
     if (!full) {
       asm volatile("");  // keeps this rare path a branch: no speculated predicates on full tiles
 #pragma unroll
@@ -592,9 +612,10 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   if (!valid) return;
   // row sum over both key halves
   const float l_run = xhalf_sum((lsum[0] + lsum[1]) + (lsum[2] + lsum[3]));
-  if (a.nsplit > 1) {
+  if (a.nsplit > 1 || kpart >= 0) {
     // partial for the combine kernel: unnormalised O, running max and sum
-    const int64_t p = (((int64_t)split * a.hkv + head) * a.tiles + tile) * ATT_BM + wv * 32 + c;
+    const int64_t p = a.nsplit > 1 ? (((int64_t)split * a.hkv + head) * a.tiles + tile) * ATT_BM + wv * 32 + c
+                                   : (((int64_t)kpart * a.hkv + head) * a.nlong + td) * ATT_BM + wv * 32 + c;
     float* po = a.ws_o + p * HD;
 #pragma unroll
     for (int d = 0; d < DB; ++d)
@@ -689,10 +710,55 @@ __global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(const AttnArg
   *reinterpret_cast<u32x2_t*>(op) = o2;
 }
 
+// Merge the two key halves of the long row tiles (nlong > 0): one wave per (KV head, row), the
+// same weighting as attn_combine_kernel for two partials.
+constexpr int HALF_ROWS = 4;  // rows (waves) per work group
+template <int HD>
+__global__ __launch_bounds__(HALF_ROWS * 64) void attn_halves_kernel(const AttnArgs a) {
+  constexpr int EPL = HD / 64;  // elements per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t per_head = (int64_t)a.nlong * ATT_BM;
+  const int64_t w = (int64_t)blockIdx.x * HALF_ROWS + (threadIdx.x >> 6);
+  if (w >= a.hkv * per_head) return;
+  const int head = (int)(w / per_head);
+  const int64_t rem = w % per_head;
+  const int td = (int)(rem / ATT_BM), rt = (int)(rem % ATT_BM);
+  const int64_t r = (int64_t)(a.tiles - 1 - td) * ATT_BM + rt;
+  if (r >= a.n * a.G) return;
+  const int64_t p0 = ((int64_t)head * a.nlong + td) * ATT_BM + rt;
+  const int64_t p1 = ((int64_t)(a.hkv + head) * a.nlong + td) * ATT_BM + rt;
+  const float m0 = a.ws_ml[p0 * 2], l0 = a.ws_ml[p0 * 2 + 1];
+  const float m1 = a.ws_ml[p1 * 2], l1 = a.ws_ml[p1 * 2 + 1];
+  const float M = fmaxf(l0 > 0.f ? m0 : -INFINITY, l1 > 0.f ? m1 : -INFINITY);
+  const float w0 = l0 > 0.f ? __builtin_amdgcn_exp2f(m0 - M) : 0.f;
+  const float w1 = l1 > 0.f ? __builtin_amdgcn_exp2f(m1 - M) : 0.f;
+  const float L = w0 * l0 + w1 * l1;
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  const float* o0 = a.ws_o + p0 * HD + lane * EPL;
+  const float* o1 = a.ws_o + p1 * HD + lane * EPL;
+  const int64_t qi = r / a.G;
+  const int qh = head * a.G + (int)(r % a.G);
+  bf16_t* op = a.out + (qi * a.hq + qh) * HD + lane * EPL;
+  if constexpr (EPL == 2) {
+    const float2 x0 = *reinterpret_cast<const float2*>(o0), x1 = *reinterpret_cast<const float2*>(o1);
+    *reinterpret_cast<uint32_t*>(op) = pack_bf((w0 * x0.x + w1 * x1.x) * inv, (w0 * x0.y + w1 * x1.y) * inv);
+  } else {
+    op[0] = f2bf((w0 * o0[0] + w1 * o1[0]) * inv);
+  }
+}
+
 struct SplitPlan {
   int nsplit, split_len;
   int64_t tiles;
+  int nlong;  // one work group per key half for the nlong longest row tiles of each KV head
 };
+
+// Row tiles per KV head run as two half-range work groups when there is no key split: a quarter
+// of them (the longest). Simulated dispatch of the recompute shape (rows sorted by position, so
+// row tile t sees about t / tiles of the context) on the 32 CUs of an XCD: 90 % of the ideal
+// makespan with whole tiles longest first, 97-98 % with the longest quarter halved and dispatched
+// first.
+constexpr int ATT_LONG_MIN_TILES = 8;
 
 static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
   SplitPlan sp;
@@ -700,6 +766,7 @@ static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
   const int64_t base = (int64_t)hkv * sp.tiles;
   sp.nsplit = 1;
   sp.split_len = 0;
+  sp.nlong = 0;
   if (base < ATT_TARGET_WGS && t_cap >= 2 * ATT_MIN_SPLIT_KEYS) {
     int64_t want = (ATT_TARGET_WGS + base - 1) / base;
     int64_t most = t_cap / ATT_MIN_SPLIT_KEYS;
@@ -712,13 +779,18 @@ static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
       sp.split_len = (int)len;
     }
   }
+  if (sp.nsplit == 1 && sp.tiles >= ATT_LONG_MIN_TILES) sp.nlong = (int)((sp.tiles + 2) / 4);
   return sp;
 }
 
+static size_t split_rows(const SplitPlan& sp, int hkv) {
+  if (sp.nsplit > 1) return (size_t)sp.nsplit * hkv * sp.tiles * ATT_BM;
+  return (size_t)2 * hkv * sp.nlong * ATT_BM;
+}
+
 static size_t split_ws_bytes(const SplitPlan& sp, int hkv, int head_dim) {
-  if (sp.nsplit <= 1) return 0;
-  size_t rows = (size_t)sp.nsplit * hkv * sp.tiles * ATT_BM;
-  return rows * (size_t)head_dim * 4 + rows * 8 + 256;
+  const size_t rows = split_rows(sp, hkv);
+  return rows ? rows * (size_t)head_dim * 4 + rows * 8 + 256 : 0;
 }
 
 }  // namespace tread
@@ -759,15 +831,20 @@ extern "C" int tread_subset_attn_bf16(const void* q, const void* k_cache, const 
   a.G = hq / hkv;
   SplitPlan sp = plan_split(n, hq, hkv, t_cap);
   const size_t need = split_ws_bytes(sp, hkv, head_dim);
-  if (sp.nsplit > 1 && (!ws || ws_bytes < need)) sp.nsplit = 1;  // no workspace: one pass per row tile
-  if (sp.tiles > 0x7fffffffLL / N_XCD) return fail(TREAD_ERANGE, "subset_attn: too many rows");
+  if (need && (!ws || ws_bytes < need)) {  // no workspace: one pass per row tile
+    sp.nsplit = 1;
+    sp.nlong = 0;
+  }
+  const int64_t vtiles = sp.tiles + sp.nlong;  // work groups per KV head without a key split
+  if (vtiles > 0x7fffffffLL / N_XCD) return fail(TREAD_ERANGE, "subset_attn: too many rows");
   a.tiles = (int32_t)sp.tiles;
   a.nsplit = sp.nsplit;
   a.split_len = sp.split_len;
-  if (sp.nsplit > 1) {
+  a.nlong = sp.nlong;
+  if (sp.nsplit > 1 || sp.nlong > 0) {
     uintptr_t base = ((uintptr_t)ws + 255) & ~(uintptr_t)255;
     a.ws_ml = (float*)base;
-    a.ws_o = a.ws_ml + (size_t)sp.nsplit * hkv * sp.tiles * ATT_BM * 2;
+    a.ws_o = a.ws_ml + split_rows(sp, hkv) * 2;
   }
   a.scale_log2 = scale * 1.4426950408889634f;
   int64_t grid;
@@ -776,10 +853,10 @@ extern "C" int tread_subset_attn_bf16(const void* q, const void* k_cache, const 
     grid = (int64_t)sp.nsplit * hkv * sp.tiles;
   } else if (hkv <= N_XCD && (N_XCD % hkv) == 0) {
     a.xpg = N_XCD / hkv;
-    grid = (int64_t)N_XCD * ((sp.tiles + a.xpg - 1) / a.xpg);
+    grid = (int64_t)N_XCD * ((vtiles + a.xpg - 1) / a.xpg);
   } else {
     a.xpg = 0;
-    grid = (int64_t)hkv * sp.tiles;
+    grid = (int64_t)hkv * vtiles;
   }
   if (grid > 0x7fffffffLL) return fail(TREAD_ERANGE, "subset_attn: grid too large");
   size_t smem = (head_dim == 128 ? AttnSmem<128>::BUF : AttnSmem<64>::BUF) * ATT_NBUF * sizeof(bf16_t);
@@ -789,7 +866,17 @@ extern "C" int tread_subset_attn_bf16(const void* q, const void* k_cache, const 
   else
     hipLaunchKernelGGL(subset_attn_kernel<64>, dim3((unsigned)grid), dim3(ATT_THREADS), smem, s, a);
   int rc = check_launch("subset_attn");
-  if (rc || sp.nsplit <= 1) return rc;
+  if (rc) return rc;
+  if (sp.nlong > 0) {
+    const int64_t rows = (int64_t)hkv * sp.nlong * ATT_BM;
+    const dim3 hgrid((unsigned)((rows + HALF_ROWS - 1) / HALF_ROWS));
+    if (head_dim == 128)
+      hipLaunchKernelGGL(attn_halves_kernel<128>, hgrid, dim3(HALF_ROWS * 64), 0, s, a);
+    else
+      hipLaunchKernelGGL(attn_halves_kernel<64>, hgrid, dim3(HALF_ROWS * 64), 0, s, a);
+    return check_launch("subset_attn halves");
+  }
+  if (sp.nsplit <= 1) return rc;
   const int64_t blocks = (int64_t)hkv * n * a.G;
   if (head_dim == 128)
     hipLaunchKernelGGL(attn_combine_kernel<128>, dim3((unsigned)blocks), dim3(CMB_THREADS), 0, s, a);
