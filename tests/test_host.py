@@ -53,9 +53,12 @@ def test_error_paths_are_reported_without_a_gpu():
     rc = lib.tread_rope_assemble_bf16(None, 1, None, None, 2, 2, 10, 128, None, 0, 2, None)
     assert rc != 0
     assert lib.tread_topk_workspace_bytes(1000) == 0
-    # split-K workspace only for few rows over a long cache
+    # split-K workspace for few rows over a long cache; key-half partials for the longest quarter
+    # of the row tiles otherwise: 6 400 rows x 7 heads = 175 row tiles per KV head, 44 of them
+    # split: 2 halves x 4 KV heads x 44 x 256 rows x (128 fp32 + max, sum) + alignment
     assert lib.tread_subset_attn_workspace_bytes(32, 28, 4, 128, 32096) > 0
-    assert lib.tread_subset_attn_workspace_bytes(6400, 28, 4, 128, 32096) == 0
+    assert lib.tread_subset_attn_workspace_bytes(6400, 28, 4, 128, 32096) == 2 * 4 * 44 * 256 * (128 * 4 + 8) + 256
+    assert lib.tread_subset_attn_workspace_bytes(64, 28, 4, 128, 200) == 0  # 2 row tiles: neither
 
 
 def test_product_kernels_refuse_cpu_tensors():
