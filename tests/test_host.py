@@ -59,6 +59,7 @@ def test_error_paths_are_reported_without_a_gpu():
     assert lib.tread_subset_attn_workspace_bytes(32, 28, 4, 128, 32096) > 0
     assert lib.tread_subset_attn_workspace_bytes(6400, 28, 4, 128, 32096) == 2 * 4 * 44 * 256 * (128 * 4 + 8) + 256
     assert lib.tread_subset_attn_workspace_bytes(64, 28, 4, 128, 200) == 0  # 2 row tiles: neither
+    assert lib.tread_subset_attn_workspace_bytes(32000, 28, 4, 128, 32096) == 0  # 3 500 work groups: balanced
 
 
 def test_product_kernels_refuse_cpu_tensors():

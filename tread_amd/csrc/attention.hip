@@ -753,12 +753,15 @@ struct SplitPlan {
   int nlong;  // one work group per key half for the nlong longest row tiles of each KV head
 };
 
-// Row tiles per KV head run as two half-range work groups when there is no key split: a quarter
-// of them (the longest). Simulated dispatch of the recompute shape (rows sorted by position, so
-// row tile t sees about t / tiles of the context) on the 32 CUs of an XCD: 90 % of the ideal
-// makespan with whole tiles longest first, 97-98 % with the longest quarter halved and dispatched
-// first.
+// Row tiles per KV head run as two half-range work groups when there is no key split and the
+// launch is a few rounds of the GPU: a quarter of them (the longest). Simulated dispatch of the
+// recompute shape (rows sorted by position, so row tile t sees about t / tiles of the context) on
+// the 32 CUs of an XCD: 90 % of the ideal makespan with whole tiles longest first, 97-98 % with
+// the longest quarter halved and dispatched first; measured 5 % faster (any quarter to two
+// fifths alike). A launch of many rounds (a 32 000-row causal pass, 3 500 work groups) is
+// balanced already and measured 1-2 % slower with halves.
 constexpr int ATT_LONG_MIN_TILES = 8;
+constexpr int64_t ATT_LONG_MAX_WGS = 1536;
 
 static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
   SplitPlan sp;
@@ -779,7 +782,7 @@ static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
       sp.split_len = (int)len;
     }
   }
-  if (sp.nsplit == 1 && sp.tiles >= ATT_LONG_MIN_TILES) sp.nlong = (int)((sp.tiles + 2) / 4);
+  if (sp.nsplit == 1 && sp.tiles >= ATT_LONG_MIN_TILES && base <= ATT_LONG_MAX_WGS) sp.nlong = (int)((sp.tiles + 2) / 4);
   return sp;
 }
 
