@@ -758,8 +758,9 @@ struct SplitPlan {
 // recompute shape (rows sorted by position, so row tile t sees about t / tiles of the context) on
 // the 32 CUs of an XCD: 90 % of the ideal makespan with whole tiles longest first, 97-98 % with
 // the longest quarter halved and dispatched first; measured 5 % faster (any quarter to two
-// fifths alike). A launch of many rounds (a 32 000-row causal pass, 3 500 work groups) is
-// balanced already and measured 1-2 % slower with halves.
+// fifths alike). Launches of more rounds are balanced already and measured slower with halves:
+// 1 % at 1 600 work groups (a 70B-shaped recompute, 8 KV heads), 1-2 % at 3 500 (a 32 000-row
+// causal pass).
 constexpr int ATT_LONG_MIN_TILES = 8;
 constexpr int64_t ATT_LONG_MAX_WGS = 1536;
 
