@@ -103,9 +103,11 @@ int tread_topk_select_bf16(const void* score, int64_t n, int64_t k, int64_t* sel
  * (tread/engine.py:206-213,257). Row i of q [n, hq, head_dim] sees cache key j of its KV head
  * iff j <= kend[i] and (j < n_shared or j >= kseg[i]); kseg may be NULL (then keys [0, kend[i]]).
  * out: [n, hq * head_dim]. scale: softmax scale (head_dim^-0.5). head_dim: 64 or 128.
- * Few rows over a long cache (the query forward) split the key axis across work groups; that needs
- * ws of tread_subset_attn_workspace_bytes(...) bytes (device). With ws NULL or too small the call
- * still succeeds, unsplit.
+ * Few rows over a long cache (the query forward) split the key axis across work groups, and a
+ * launch of a few GPU rounds (the recompute rows) runs the longest quarter of its row tiles as two
+ * key-half work groups; both keep fp32 partials in ws of tread_subset_attn_workspace_bytes(...)
+ * bytes (device) and merge them in a second kernel. With ws NULL or too small the call still
+ * succeeds, with whole row tiles and no key split.
  */
 size_t tread_subset_attn_workspace_bytes(int64_t n, int hq, int hkv, int head_dim, int64_t t_cap);
 int tread_subset_attn_bf16(const void* q, const void* k_cache, const void* v_cache, const int64_t* kend,

@@ -318,6 +318,22 @@ def test_topk_select_handles_negative_and_distinct_scores():
 
 # ------------------------------------------------------------------------------------------- (c)
 
+def ref_attention_rounded(q, K, V, kend, scale):
+    """The causal attention with the kernel's rounding points: q scaled by scale * log2(e) and
+    rounded to bf16, fp32 scores, P = exp2(s - row max) rounded to bf16 for P V, fp32 sum."""
+    n, hq, hd = q.shape
+    hkv, t_cap, _ = K.shape
+    G = hq // hkv
+    vis = torch.arange(t_cap)[None, :] <= kend[:, None]
+    out = torch.empty(n, hq, hd)
+    for h in range(hq):
+        qs = (q[:, h].float() * (scale * 1.4426950408889634)).to(torch.bfloat16).float()
+        s = (qs @ K[h // G].float().T).masked_fill(~vis, -float("inf"))
+        p = torch.exp2(s - s.max(-1, keepdim=True).values)
+        out[:, h] = (p.to(torch.bfloat16).float() @ V[h // G].float()) / p.sum(-1, keepdim=True)
+    return out
+
+
 def ref_attention(q, K, V, kend, scale, kseg=None, n_shared=0):
     """Textbook masked GQA softmax attention in fp32 on the CPU. q [n, hq, hd], K/V [hkv, T, hd]."""
     n, hq, hd = q.shape
@@ -351,6 +367,9 @@ CASES = [
     (28, 4, 128, 1000, 1000, "subset"),
     (28, 4, 128, 1000, 1000, "prefill"),
     (14, 2, 64, 1000, 900, "segments"),
+    # the same with a few late keys scaled up: row maxima move by far more than 2^8 in later key
+    # tiles, so the lazy rescale fires inside the key halves and the merge sees different maxima
+    (28, 4, 128, 1000, 1000, "spikes"),
     # few rows over a long cache: split-K + combine
     (28, 4, 128, 20000, 32, "query"),
     (14, 2, 64, 9000, 5, "query"),
@@ -366,7 +385,11 @@ def test_subset_attention_vs_textbook(hq, hkv, hd, t_cap, n, kind):
     K = torch.randn(hkv, t_cap, hd, generator=g).to(torch.bfloat16)
     V = torch.randn(hkv, t_cap, hd, generator=g).to(torch.bfloat16)
     kseg, n_shared = None, 0
-    if kind == "subset":
+    if kind == "spikes":
+        kend = torch.sort(torch.randperm(t_cap, generator=g)[:n]).values
+        hot = torch.randperm(t_cap // 2, generator=g)[:8] + t_cap // 2
+        K[:, hot] = (K[:, hot].float() * 6).to(torch.bfloat16)
+    elif kind == "subset":
         kend = torch.sort(torch.randperm(t_cap, generator=g)[:n]).values
     elif kind == "prefill":
         kend = torch.arange(n)
@@ -383,6 +406,14 @@ def test_subset_attention_vs_textbook(hq, hkv, hd, t_cap, n, kind):
                            kseg=None if kseg is None else kseg.to(DEV), n_shared=n_shared)
     got = out.cpu().float().view(n, hq, hd)
     err = (got - ref).abs()
+    if kind == "spikes":
+        # The kernel's roundings (q pre-multiplied by scale * log2(e) in bf16, P in bf16 for P V,
+        # fp32 sums) already move the textbook result by up to 0.04 on 6x-scaled keys; against
+        # that rounding model the kernel must agree closely, whatever its running maxima did.
+        emu = ref_attention_rounded(q, K, V, kend, scale)
+        assert (got - emu).abs().max().item() < 2e-2, (got - emu).abs().max()
+        assert err.max().item() < 6e-2 and err.mean().item() < 3e-3, (err.max(), err.mean())
+        return
     assert err.max().item() < 3e-2, err.max()
     assert err.mean().item() < 3e-3, err.mean()
 
