@@ -176,7 +176,9 @@ def test_silu_mul_vs_torch():
 @pytest.mark.parametrize("m,n,k,bias,ldx", [(1, 32, 256, False, 256), (8, 4608, 3584, True, 3584),
                                              (3, 96, 512, True, 640), (32, 3584, 4608, False, 4608),
                                              (17, 1024, 4096, False, 4096), (8, 3584, 18944, False, 18944),
-                                             (1, 37888, 3584, False, 3584), (5, 32, 16384, True, 16384)])
+                                             (1, 37888, 3584, False, 3584), (5, 32, 16384, True, 16384),
+                                             (2, 2048, 2048, True, 2056), (2, 96, 16384, False, 16384),
+                                             (1, 3584, 18944, True, 18944)])
 def test_skinny_linear_matches_fp32_reference(m, n, k, bias, ldx):
     """y = x W^T (+ b) of a few rows against the fp32 product of the same bf16 values: within one
     bf16 ulp of it plus the fp32 reordering error (1e-5 of the sum of |terms|, which matters only
@@ -202,10 +204,14 @@ def test_skinny_linear_splits_k_for_few_features():
     assert _hip.lib().tread_skinny_workspace_bytes(1, 37888, 3584) == 0  # many features
     assert _hip.lib().tread_skinny_workspace_bytes(8, 3584, 3584) == 0  # short K
     assert _hip.lib().tread_skinny_workspace_bytes(5, 32, 16384) == 4 * 5 * 32 * 4
+    # one or two rows take 16-feature tiles below 128 tiles of 32: twice the work groups, fewer splits
+    assert _hip.lib().tread_skinny_workspace_bytes(1, 3584, 18944) == 2 * 1 * 3584 * 4
+    assert _hip.lib().tread_skinny_workspace_bytes(2, 96, 16384) == 4 * 2 * 96 * 4
 
 
 @pytest.mark.parametrize("m,H,n,with_delta,bias", [(1, 3584, 4608, True, True), (8, 512, 1536, True, False),
-                                                     (3, 256, 96, False, False)])
+                                                     (3, 256, 96, False, False), (2, 3584, 3584, True, True),
+                                                     (1, 896, 1152, False, True)])
 def test_skinny_norm_linear_equals_norm_then_linear(m, H, n, with_delta, bias):
     """The fused norm prologue gives add_rmsnorm's bits: its output equals skinny_linear applied
     to add_rmsnorm's output bit for bit, and h_out equals add_rmsnorm's sum."""

@@ -2,22 +2,24 @@
 // and out, fp32 accumulation, M <= 32. Memory-bound: every weight byte is read once from HBM, so
 // the kernel is built to keep enough 16-byte weight loads in flight.
 //
-// One work group of 8 waves per 32 output features. Each wave walks its 1/8 of K with
+// One work group of 8 waves per TN = 32 (or 16) output features. Each wave walks its 1/8 of K with
 // v_mfma_f32_32x32x16_bf16: A = 32 weight rows x 16 K (lane l: row l % 32, 8 consecutive K at
 // (l / 32) * 8 -- one 16-byte load), B = the token rows as columns (lane l: token l % 32, the same
-// 8 K; tokens >= M load nothing and stay zero). The 8 partial 32 x 32 tiles meet in LDS, and one
-// thread per (token, feature) sums them, adds the bias and rounds once to bf16 (as F.linear does).
-// A layer with few output features (fewer than 448 such work groups) and a long K also splits K
-// across 2, 4 or 8 work groups per tile: their fp32 sums meet in a workspace, and a second small
-// kernel adds them and the bias and rounds once.
+// 8 K; tokens >= M load nothing and stay zero); with TN = 16 the same with v_mfma_f32_16x16x32_bf16
+// (lane l: row / token l % 16, K at (l / 16) * 8 of a 32-K step). The 8 partial TN x TN tiles meet
+// in LDS, and one thread per (token, feature) sums them, adds the bias and rounds once to bf16 (as
+// F.linear does). A layer with few output features (fewer than 448 such work groups) and a long K
+// also splits K across 2, 4 or 8 work groups per tile: their fp32 sums meet in a workspace, and a
+// second small kernel adds them and the bias and rounds once.
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/tread_hip.h"
 
 namespace tread {
 
 constexpr int SK_WAVES = 8;
-constexpr int SK_ROWS = 32;  // output features per work group
-constexpr int SK_U = 4;      // K steps (16 each) whose loads are issued together
+constexpr int SK_U = 4;  // MFMA K steps whose loads are issued together
 
 enum { PRO_NONE = 0, PRO_NORM = 1, PRO_SILU = 2 };
 
@@ -42,44 +44,53 @@ struct SkinnyArgs {
 // PRO_NORM stages norm(h + delta) of the M rows in LDS first (add_rmsnorm_row: the same bits as
 // the stand-alone add + RMSNorm kernel) and work group (0, 0) writes h + delta to h_out; PRO_SILU
 // stages this work group's K slice of bf16(bf16(silu(g)) * u) (the same bits as silu_mul_kernel).
-template <int PRO, int CPT>
+template <int PRO, int CPT, int TN>
 __global__ __launch_bounds__(SK_WAVES * 64) void skinny_gemm_kernel(const SkinnyArgs a) {
+  static_assert(TN == 32 || TN == 16, "tile of 32 or 16 features");
+  constexpr int KSTEP = 512 / TN;     // K per MFMA: 16 (32 x 32 x 16) or 32 (16 x 16 x 32)
+  constexpr int NACC = TN * TN / 64;  // accumulator registers per lane
+  using acc_t = std::conditional_t<TN == 32, f32x16_t, f32x4_t>;
   extern __shared__ __align__(16) bf16_t xs[];  // staged operand rows (PRO_NORM / PRO_SILU)
-  __shared__ float red[SK_WAVES][16][64];
+  __shared__ float red[SK_WAVES][NACC][64];
   __shared__ float nred[32];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int r32 = lane & 31, half = lane >> 5;
+  const int rt = lane % TN, kg = lane / TN;  // weight row and token of the tile; group of 8 K
   const int M = a.M, K = a.K;
-  const int64_t n0 = (int64_t)blockIdx.x * SK_ROWS;
+  const int64_t n0 = (int64_t)blockIdx.x * TN;
   const int ks = gridDim.y, q = blockIdx.y;
   const int kslice = K / ks, k0 = q * kslice;
-  const int kw = kslice / SK_WAVES;  // a multiple of 16
-  const int kb = k0 + wv * kw + half * 8;  // this lane's first K
-  const bf16_t* wp = a.w + (n0 + r32) * (int64_t)K + kb;
-  const bool xon = r32 < M;
-  const int xrow = xon ? r32 : 0;
+  const int kw = kslice / SK_WAVES;  // a multiple of KSTEP
+  const int kb = k0 + wv * kw + kg * 8;  // this lane's first K
+  const bf16_t* wp = a.w + (n0 + rt) * (int64_t)K + kb;
+  const bool xon = rt < M;
+  const int xrow = xon ? rt : 0;
   const u32x4_t zero = {0u, 0u, 0u, 0u};
-  f32x16_t acc = {};
-  const int steps = kw / 16;
+  acc_t acc = {};
+  const int steps = kw / KSTEP;
+  auto mma = [](u32x4_t av, u32x4_t bv, acc_t c) {
+    if constexpr (TN == 32)
+      return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
+                                                     c, 0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
+                                                     c, 0, 0, 0);
+  };
 
   auto mainloop = [&](const bf16_t* xp) {
     int s = 0;
     for (; s + SK_U <= steps; s += SK_U) {
       u32x4_t av[SK_U], bv[SK_U];
 #pragma unroll
-      for (int u = 0; u < SK_U; ++u) av[u] = *reinterpret_cast<const u32x4_t*>(wp + (s + u) * 16);
+      for (int u = 0; u < SK_U; ++u) av[u] = *reinterpret_cast<const u32x4_t*>(wp + (s + u) * KSTEP);
 #pragma unroll
-      for (int u = 0; u < SK_U; ++u) bv[u] = xon ? *reinterpret_cast<const u32x4_t*>(xp + (s + u) * 16) : zero;
+      for (int u = 0; u < SK_U; ++u) bv[u] = xon ? *reinterpret_cast<const u32x4_t*>(xp + (s + u) * KSTEP) : zero;
 #pragma unroll
-      for (int u = 0; u < SK_U; ++u)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, av[u]),
-                                                      __builtin_bit_cast(bf16x8_t, bv[u]), acc, 0, 0, 0);
+      for (int u = 0; u < SK_U; ++u) acc = mma(av[u], bv[u], acc);
     }
     for (; s < steps; ++s) {
-      const u32x4_t av = *reinterpret_cast<const u32x4_t*>(wp + s * 16);
-      const u32x4_t bv = xon ? *reinterpret_cast<const u32x4_t*>(xp + s * 16) : zero;
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
-                                                    acc, 0, 0, 0);
+      const u32x4_t av = *reinterpret_cast<const u32x4_t*>(wp + s * KSTEP);
+      const u32x4_t bv = xon ? *reinterpret_cast<const u32x4_t*>(xp + s * KSTEP) : zero;
+      acc = mma(av, bv, acc);
     }
   };
 
@@ -108,12 +119,14 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_gemm_kernel(const Skinny
     mainloop(xs + xrow * kslice + (kb - k0));
   }
 #pragma unroll
-  for (int r = 0; r < 16; ++r) red[wv][r][lane] = acc[r];
+  for (int r = 0; r < NACC; ++r) red[wv][r][lane] = acc[r];
   __syncthreads();
-  // C layout: lane l holds column (token) l % 32; register r holds row (r / 4) * 8 + (l / 32) * 4 + r % 4
-  for (int t = threadIdx.x; t < SK_ROWS * M; t += SK_WAVES * 64) {
-    const int m = t / SK_ROWS, row = t % SK_ROWS;
-    const int r = (row >> 3) * 4 + (row & 3), ln = m + 32 * ((row >> 2) & 1);
+  // C layout: lane l holds column (token) l % TN; register r holds row (r / 4) * 8 + (l / 32) * 4 + r % 4
+  // of the 32 x 32 tile, row (l / 16) * 4 + r of the 16 x 16 tile
+  for (int t = threadIdx.x; t < TN * M; t += SK_WAVES * 64) {
+    const int m = t / TN, row = t % TN;
+    const int r = TN == 32 ? (row >> 3) * 4 + (row & 3) : (row & 3);
+    const int ln = TN == 32 ? m + 32 * ((row >> 2) & 1) : m + 16 * (row >> 2);
     float v = 0.f;
 #pragma unroll
     for (int p = 0; p < SK_WAVES; ++p) v += red[p][r][ln];
@@ -138,16 +151,25 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
   y[(int64_t)m * ldy + n] = f2bf(v);
 }
 
-// K slices per 32-feature tile: enough work groups to cover the GPU when the feature count is small,
-// as long as every wave keeps at least 32 steps of 16 (shorter slices measured slower than one
-// work group per tile) and K splits into whole steps.
-static int skinny_ksplit(int64_t m, int64_t n, int64_t k) {
-  const int64_t tiles = n / SK_ROWS;
+// Tile width: 16 features (twice the work groups, 64 contiguous weight bytes per row per step) for
+// one or two rows and fewer than 128 tiles of 32, measured faster there at one row: 11-17 % on a 7B
+// model's down projection (3 584 x 18 944, with and without the SiLU prologue) and 8 % on o
+// (3 584 x 3 584); 32 elsewhere (at 144 tiles the norm prologue, repeated by twice the work groups,
+// made 16 slower; so did the SiLU prologue at 4 and 8 rows). The choice depends on the shape alone,
+// so the fused prologues give the plain kernel's bits.
+static int skinny_tn(int64_t m, int64_t n, int64_t k) {
+  return (m <= 2 && n / 32 < 128 && (k % (SK_WAVES * 32)) == 0) ? 16 : 32;
+}
+
+// K slices per tile: enough work groups to cover the GPU when the feature count is small, as long
+// as every wave keeps at least 512 K (shorter slices measured slower than one work group per tile)
+// and K splits into whole MFMA steps.
+static int skinny_ksplit(int tn, int64_t n, int64_t k) {
+  const int64_t tiles = n / tn, kstep = 512 / tn;
   int ks = 1;
-  while (ks < 8 && tiles * ks < 448 && (k % ((int64_t)SK_WAVES * 16 * ks * 2)) == 0 &&
-         k / ((int64_t)SK_WAVES * 16 * ks * 2) >= 32)
+  while (ks < 8 && tiles * ks < 448 && (k % ((int64_t)SK_WAVES * kstep * ks * 2)) == 0 &&
+         k / ((int64_t)SK_WAVES * ks * 2) >= 512)
     ks *= 2;
-  (void)m;
   return ks;
 }
 
@@ -155,14 +177,20 @@ static int skinny_ksplit(int64_t m, int64_t n, int64_t k) {
 
 using namespace tread;
 
-static int launch_skinny(int pro, int cpt, const SkinnyArgs& a, int ks, size_t lds, hipStream_t s) {
-  const dim3 grid((unsigned)(a.N / SK_ROWS), (unsigned)ks), block(SK_WAVES * 64);
-  if (pro == PRO_NONE) hipLaunchKernelGGL((skinny_gemm_kernel<PRO_NONE, 1>), grid, block, lds, s, a);
-  else if (pro == PRO_SILU) hipLaunchKernelGGL((skinny_gemm_kernel<PRO_SILU, 1>), grid, block, lds, s, a);
-  else if (cpt <= 1) hipLaunchKernelGGL((skinny_gemm_kernel<PRO_NORM, 1>), grid, block, lds, s, a);
-  else if (cpt <= 2) hipLaunchKernelGGL((skinny_gemm_kernel<PRO_NORM, 2>), grid, block, lds, s, a);
-  else if (cpt <= 4) hipLaunchKernelGGL((skinny_gemm_kernel<PRO_NORM, 4>), grid, block, lds, s, a);
-  else hipLaunchKernelGGL((skinny_gemm_kernel<PRO_NORM, 8>), grid, block, lds, s, a);
+template <int PRO, int CPT>
+static void launch_tile(int tn, dim3 grid, size_t lds, hipStream_t s, const SkinnyArgs& a) {
+  if (tn == 16) hipLaunchKernelGGL((skinny_gemm_kernel<PRO, CPT, 16>), grid, dim3(SK_WAVES * 64), lds, s, a);
+  else hipLaunchKernelGGL((skinny_gemm_kernel<PRO, CPT, 32>), grid, dim3(SK_WAVES * 64), lds, s, a);
+}
+
+static int launch_skinny(int pro, int cpt, int tn, const SkinnyArgs& a, int ks, size_t lds, hipStream_t s) {
+  const dim3 grid((unsigned)(a.N / tn), (unsigned)ks);
+  if (pro == PRO_NONE) launch_tile<PRO_NONE, 1>(tn, grid, lds, s, a);
+  else if (pro == PRO_SILU) launch_tile<PRO_SILU, 1>(tn, grid, lds, s, a);
+  else if (cpt <= 1) launch_tile<PRO_NORM, 1>(tn, grid, lds, s, a);
+  else if (cpt <= 2) launch_tile<PRO_NORM, 2>(tn, grid, lds, s, a);
+  else if (cpt <= 4) launch_tile<PRO_NORM, 4>(tn, grid, lds, s, a);
+  else launch_tile<PRO_NORM, 8>(tn, grid, lds, s, a);
   int rc = check_launch("skinny_linear");
   if (rc || ks <= 1) return rc;
   const int64_t total = (int64_t)a.M * a.N;
@@ -172,15 +200,15 @@ static int launch_skinny(int pro, int cpt, const SkinnyArgs& a, int ks, size_t l
 }
 
 // Dynamic LDS the staged operand rows may take: gfx950's 160 KiB per work group less the kernel's
-// static arrays (partial tiles 32 KiB, norm scratch) and some headroom.
+// static arrays (partial tiles of the 32-feature tile, 32 KiB; norm scratch) and some headroom.
 constexpr size_t SK_STAGE_MAX = 160 * 1024 - sizeof(float) * (SK_WAVES * 16 * 64 + 32) - 256;
 
 // K slices of the SiLU-gated projection: the plain rule, then more slices until this work group's
 // staged rows fit in LDS (0: no split fits).
-static int silu_ksplit(int64_t m, int64_t n, int64_t k) {
-  int ks = skinny_ksplit(m, n, k);
+static int silu_ksplit(int tn, int64_t m, int64_t n, int64_t k) {
+  int ks = skinny_ksplit(tn, n, k);
   while ((size_t)m * (k / ks) * sizeof(bf16_t) > SK_STAGE_MAX) {
-    if (ks >= 64 || (k % ((int64_t)SK_WAVES * 16 * ks * 2)) != 0) return 0;
+    if (ks >= 64 || (k % ((int64_t)SK_WAVES * (512 / tn) * ks * 2)) != 0) return 0;
     ks *= 2;
   }
   return ks;
@@ -189,22 +217,22 @@ static int silu_ksplit(int64_t m, int64_t n, int64_t k) {
 static int check_shape(const char* what, int64_t m, int64_t mmax, int64_t n, int64_t k) {
   if (m < 0 || m > mmax || n < 0 || k <= 0)
     return fail(TREAD_EINVAL, "%s: bad shape (m=%lld n=%lld k=%lld)", what, (long long)m, (long long)n, (long long)k);
-  if ((n % SK_ROWS) != 0 || (k % (SK_WAVES * 16)) != 0)
-    return fail(TREAD_EINVAL, "%s: n=%lld must be a multiple of %d and k=%lld of %d", what, (long long)n, SK_ROWS,
+  if ((n % 32) != 0 || (k % (SK_WAVES * 16)) != 0)
+    return fail(TREAD_EINVAL, "%s: n=%lld must be a multiple of 32 and k=%lld of %d", what, (long long)n,
                 (long long)k, SK_WAVES * 16);
-  if (n / SK_ROWS > 0x7fffffffLL || k > 0x7fffffffLL) return fail(TREAD_ERANGE, "%s: too large", what);
+  if (n / 16 > 0x7fffffffLL || k > 0x7fffffffLL) return fail(TREAD_ERANGE, "%s: too large", what);
   return 0;
 }
 
 extern "C" size_t tread_skinny_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-  if (m <= 0 || m > 32 || n <= 0 || (n % SK_ROWS) != 0 || k <= 0 || (k % (SK_WAVES * 16)) != 0) return 0;
-  const int ks = skinny_ksplit(m, n, k);
+  if (m <= 0 || m > 32 || n <= 0 || (n % 32) != 0 || k <= 0 || (k % (SK_WAVES * 16)) != 0) return 0;
+  const int ks = skinny_ksplit(skinny_tn(m, n, k), n, k);
   return ks > 1 ? (size_t)ks * m * n * sizeof(float) : 0;
 }
 
 extern "C" size_t tread_skinny_silu_workspace_bytes(int64_t m, int64_t n, int64_t inter) {
-  if (m <= 0 || m > 8 || n <= 0 || (n % SK_ROWS) != 0 || inter <= 0 || (inter % (SK_WAVES * 16)) != 0) return 0;
-  const int ks = silu_ksplit(m, n, inter);
+  if (m <= 0 || m > 8 || n <= 0 || (n % 32) != 0 || inter <= 0 || (inter % (SK_WAVES * 16)) != 0) return 0;
+  const int ks = silu_ksplit(skinny_tn(m, n, inter), m, n, inter);
   return ks > 1 ? (size_t)ks * m * n * sizeof(float) : 0;
 }
 
@@ -216,7 +244,8 @@ extern "C" int tread_skinny_linear_bf16(const void* x, int64_t ldx, const void* 
   if (!x || !weight || !y) return fail(TREAD_EINVAL, "skinny_linear: null pointer");
   if (ldx < k || ldy < n || (ldx % 8) != 0) return fail(TREAD_EINVAL, "skinny_linear: bad leading dimensions");
   if ((((uintptr_t)x | (uintptr_t)weight) & 15) != 0) return fail(TREAD_EINVAL, "skinny_linear: x/weight not 16-byte aligned");
-  int ks = skinny_ksplit(m, n, k);
+  const int tn = skinny_tn(m, n, k);
+  int ks = skinny_ksplit(tn, n, k);
   if (ks > 1 && (!ws || ws_bytes < (size_t)ks * m * n * sizeof(float) || (((uintptr_t)ws) & 15) != 0)) ks = 1;
   SkinnyArgs a;
   memset(&a, 0, sizeof(a));
@@ -230,7 +259,7 @@ extern "C" int tread_skinny_linear_bf16(const void* x, int64_t ldx, const void* 
   a.M = (int)m;
   a.K = (int)k;
   a.N = (int)n;
-  return launch_skinny(PRO_NONE, 1, a, ks, 0, (hipStream_t)stream);
+  return launch_skinny(PRO_NONE, 1, tn, a, ks, 0, (hipStream_t)stream);
 }
 
 extern "C" int tread_skinny_norm_linear_bf16(const void* h, const void* delta, const void* ln_weight, float eps,
@@ -260,7 +289,7 @@ extern "C" int tread_skinny_norm_linear_bf16(const void* h, const void* delta, c
   a.K = (int)k;
   a.N = (int)n;
   const int nthr = rmsnorm_threads((int)k), cpt = (int)((k / 8 + nthr - 1) / nthr);
-  return launch_skinny(PRO_NORM, cpt, a, 1, (size_t)m * k * sizeof(bf16_t), (hipStream_t)stream);
+  return launch_skinny(PRO_NORM, cpt, skinny_tn(m, n, k), a, 1, (size_t)m * k * sizeof(bf16_t), (hipStream_t)stream);
 }
 
 extern "C" int tread_skinny_silu_linear_bf16(const void* gate_up, int64_t m, int64_t inter, const void* weight,
@@ -270,7 +299,8 @@ extern "C" int tread_skinny_silu_linear_bf16(const void* gate_up, int64_t m, int
   if (!gate_up || !weight || !y) return fail(TREAD_EINVAL, "skinny_silu_linear: null pointer");
   if ((((uintptr_t)gate_up | (uintptr_t)weight) & 15) != 0)
     return fail(TREAD_EINVAL, "skinny_silu_linear: operands not 16-byte aligned");
-  const int ks = silu_ksplit(m, n, inter);
+  const int tn = skinny_tn(m, n, inter);
+  const int ks = silu_ksplit(tn, m, n, inter);
   if (ks == 0) return fail(TREAD_EINVAL, "skinny_silu_linear: %lld rows of %lld do not fit in LDS", (long long)m,
                            (long long)inter);
   if (ks > 1 && (!ws || ws_bytes < (size_t)ks * m * n * sizeof(float) || (((uintptr_t)ws) & 15) != 0))
@@ -287,5 +317,5 @@ extern "C" int tread_skinny_silu_linear_bf16(const void* gate_up, int64_t m, int
   a.M = (int)m;
   a.K = (int)inter;
   a.N = (int)n;
-  return launch_skinny(PRO_SILU, 1, a, ks, (size_t)m * (inter / ks) * sizeof(bf16_t), (hipStream_t)stream);
+  return launch_skinny(PRO_SILU, 1, tn, a, ks, (size_t)m * (inter / ks) * sizeof(bf16_t), (hipStream_t)stream);
 }
