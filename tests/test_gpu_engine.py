@@ -134,7 +134,7 @@ def test_keys_stats_and_logits_match_oracle_across_ratios(setup):
 
 @pytest.mark.parametrize("name", list(CFGS))
 def test_logits_within_kl_1e4_at_benchmark_init(name):
-    """The north-star bar at the benchmark's N(0, 0.02) weights: KL(reference bf16, ours) < 1e-4
+    """The logits tolerance at the benchmark's N(0, 0.02) weights: KL(reference bf16, ours) < 1e-4
     for plain reuse and 20% / 50% deviation recompute."""
     cfg, gpu, ref = build(name, std=0.02)
     prefix, docs, query = request(cfg, seed=21)
@@ -437,7 +437,7 @@ def test_decode_matches_oracle_generation_step_by_step(setup, graphs, ratio, res
 
 @pytest.mark.parametrize("name", list(CFGS))
 def test_decode_within_kl_1e4_at_benchmark_init(name):
-    """The north-star bar on every decode step at the benchmark's N(0, 0.02) weights:
+    """The logits tolerance on every decode step at the benchmark's N(0, 0.02) weights:
     KL(reference bf16, ours) < 1e-4 (graph steps after a 20% recompute)."""
     cfg, gpu, ref = build(name, std=0.02)
     prefix, docs, query = request(cfg, seed=22)

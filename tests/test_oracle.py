@@ -428,7 +428,7 @@ def test_blend_with_no_docs_and_zero_budget(om):
 
 # ---------------------------------------------------------------------------- the reference's CPU case
 
-def test_config1_cpu_fp32_reversed_reuse():
+def test_small_model_cpu_fp32_reversed_reuse_of_4_docs():
     """Qwen2.5-0.5B-shaped fp32 model (24 layers, hidden 896, 14/2 heads, head_dim 64, theta 1e6,
     vocab 151936), 64-token system prompt + 4 docs x 256 + 32-token query; docs cached in order
     1..4, then reassembled in reversed order with plain reuse: all 5 blocks hit, and every doc's
