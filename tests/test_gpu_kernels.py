@@ -205,7 +205,7 @@ def test_skinny_linear_splits_k_for_few_features():
     assert _hip.lib().tread_skinny_workspace_bytes(8, 3584, 3584) == 0  # short K
     assert _hip.lib().tread_skinny_workspace_bytes(5, 32, 16384) == 4 * 5 * 32 * 4
     # one or two rows take 16-feature tiles below 128 tiles of 32: twice the work groups, fewer splits
-    assert _hip.lib().tread_skinny_workspace_bytes(1, 3584, 18944) == 2 * 1 * 3584 * 4
+    assert _hip.lib().tread_skinny_workspace_bytes(1, 3584, 18944) == 0  # 224 groups: unsplit
     assert _hip.lib().tread_skinny_workspace_bytes(2, 96, 16384) == 4 * 2 * 96 * 4
 
 
