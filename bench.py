@@ -24,6 +24,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "reuse TTFT ms @32k ctx, 20% recompute; re-rotate+assemble GB/s (% HBM peak)"
 HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 # HBM bytes per assemble launch, from two rocprofv3 PMC passes on this workload (FETCH_SIZE x 2.0,
 # WRITE_SIZE x 1.0: the factors a plain copy of known size reads on MI355X); the profiler cannot
 # run inside this process, so the figure is carried here for the workload it was measured on.
@@ -99,6 +100,36 @@ def time_assemble(eng, system, docs, order, n_query, iters=20):
     sec = e0.elapsed_time(e1) / 1e3 / iters
     nbytes = 2 * 2 * (T * P.L * P.hkv * P.hd * 2)  # read + write, K and V
     return sec, nbytes
+
+
+def time_recompute_attention(eng, S, T, n_query, iters=20):
+    """The recompute attention of the request alone: the selected rows S and the query rows
+    (positions T..T+n_query-1) over a cache of T + n_query rows, as one recompute layer launches
+    it (subset_attn_kernel, plus attn_halves_kernel when the longest row tiles run as key halves),
+    timed with HIP events on the stream it runs on. Inputs are random (the time does not depend on
+    the values). Returns (avg seconds per call, FLOP per call: 4 hq hd sum(keys per row))."""
+    from tread_amd import _hip
+    P = eng.P
+    dev = S.device
+    rows = torch.cat([S.to(torch.int64), torch.arange(T, T + n_query, device=dev)])
+    n, t_cap = rows.numel(), T + n_query
+    g = torch.Generator(device=dev).manual_seed(5)
+    q = torch.randn(n, P.hq, P.hd, device=dev, dtype=torch.bfloat16, generator=g)
+    K = torch.randn(1, P.hkv, t_cap, P.hd, device=dev, dtype=torch.bfloat16, generator=g)
+    V = torch.randn(1, P.hkv, t_cap, P.hd, device=dev, dtype=torch.bfloat16, generator=g)
+    out = torch.empty(n, P.hq * P.hd, device=dev, dtype=torch.bfloat16)
+    _hip.subset_attn(q, K, V, rows, P.hq, P.hkv, P.hd, P.scale, out=out)  # warm
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(iters):
+        _hip.subset_attn(q, K, V, rows, P.hq, P.hkv, P.hd, P.scale, out=out)
+    e1.record(s)
+    e1.synchronize()
+    sec = e0.elapsed_time(e1) / 1e3 / iters
+    flop = 4 * P.hq * P.hd * float((rows.double() + 1).sum())
+    return sec, flop
 
 
 def time_decode(eng, system, docs, query, ratio, n):
@@ -310,11 +341,19 @@ def main():
                 f"{1 + n_docs} blocks (promoted by H2D; evictions reuse the pinned copies"
                 f"{', files are written once' if args.disk_tier else ''})")
         log(f"[bench] timed: median ttft {statistics.median(ttfts) * 1e3:.1f} ms, wall/step {wall * 1e3:.1f} ms")
+        attn = None
         if eng.last_selected is not None:
             S = eng.last_selected.double()
             flop = 4 * cfg.num_attention_heads * cfg.head_dim * float((S + 1).sum())
             log(f"[bench] recompute: {S.numel()} rows, mean position {float(S.mean()):.0f}, "
                 f"attention {flop:.3e} FLOP per layer")
+            a_sec, a_flop = time_recompute_attention(eng, eng.last_selected, T, n_query)
+            a_tf = a_flop / a_sec / 1e12
+            log(f"[bench] recompute attention (selected + query rows): {a_sec * 1e6:.1f} us, {a_tf:.0f} TFLOP/s")
+            attn = {"bound": "mfma", "kernel": "tread::subset_attn_kernel (+ attn_halves_kernel)",
+                    "achieved": round(a_tf, 1), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(a_tf / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                    "avg_us": round(a_sec * 1e6, 2), "algorithmic_flop": a_flop}
         full_ms = None
         if args.full_reps > 0:
             prefill_full(model, system, order, query)
@@ -359,6 +398,7 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": MEASURED_ASSEMBLE_TRAFFIC.get(args.workload), "avg_us": round(sec * 1e6, 2),
                      "algorithmic_bytes": nbytes},
+        "roofline_recompute_attention": attn,
         "cpu_baseline": cpu,
         "decode": decode,
     }
