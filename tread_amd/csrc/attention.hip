@@ -747,6 +747,53 @@ __global__ __launch_bounds__(HALF_ROWS * 64) void attn_halves_kernel(const AttnA
   }
 }
 
+// Merge split-K partials of launches with few key slices (nsplit <= CMB_FEW_SPLITS): one wave per
+// (KV head, row), each lane owning HD / 64 output elements, the slices walked in order. Same
+// weights as attn_combine_kernel (exp2(m_s - M), empty slices skipped). One wave per row instead of
+// a 256-thread work group: a 1.5B-shaped recompute (3 232 rows, 12 / 2 heads, 16 096 keys, 4 slices)
+// measured 321 -> 292 us per attention call, a 0.5B-shaped one (1 632 rows, 6 slices) 108 -> 90 us.
+constexpr int CMB_FEW_SPLITS = 8;
+template <int HD>
+__global__ __launch_bounds__(HALF_ROWS * 64) void attn_combine_few_kernel(const AttnArgs a) {
+  constexpr int EPL = HD / 64;  // elements per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t R = a.n * a.G;
+  const int64_t w = (int64_t)blockIdx.x * HALF_ROWS + (threadIdx.x >> 6);
+  if (w >= (int64_t)a.hkv * R) return;
+  const int head = (int)(w / R);
+  const int64_t r = w % R;
+  const int tile = (int)(r / ATT_BM), in_tile = (int)(r % ATT_BM);
+  const int64_t stride = (int64_t)a.hkv * a.tiles * ATT_BM;
+  const int64_t p0 = ((int64_t)head * a.tiles + tile) * ATT_BM + in_tile;
+  float M = -INFINITY;
+  for (int sp = 0; sp < a.nsplit; ++sp) {
+    const int64_t p = p0 + sp * stride;
+    if (a.ws_ml[p * 2 + 1] > 0.f) M = fmaxf(M, a.ws_ml[p * 2]);
+  }
+  float L = 0.f, acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+  for (int sp = 0; sp < a.nsplit; ++sp) {
+    const int64_t p = p0 + sp * stride;
+    const float l = a.ws_ml[p * 2 + 1];
+    if (!(l > 0.f)) continue;
+    const float wgt = __builtin_amdgcn_exp2f(a.ws_ml[p * 2] - M);
+    L += wgt * l;
+    const float* o = a.ws_o + p * HD + lane * EPL;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] += wgt * o[e];
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  const int64_t qi = r / a.G;
+  const int qh = head * a.G + (int)(r % a.G);
+  bf16_t* op = a.out + (qi * a.hq + qh) * HD + lane * EPL;
+  if constexpr (EPL == 2) {
+    *reinterpret_cast<uint32_t*>(op) = pack_bf(acc[0] * inv, acc[1] * inv);
+  } else {
+    op[0] = f2bf(acc[0] * inv);
+  }
+}
+
 struct SplitPlan {
   int nsplit, split_len;
   int64_t tiles;
@@ -882,6 +929,14 @@ extern "C" int tread_subset_attn_bf16(const void* q, const void* k_cache, const 
   }
   if (sp.nsplit <= 1) return rc;
   const int64_t blocks = (int64_t)hkv * n * a.G;
+  if (sp.nsplit <= CMB_FEW_SPLITS) {
+    const dim3 fgrid((unsigned)((blocks + HALF_ROWS - 1) / HALF_ROWS));
+    if (head_dim == 128)
+      hipLaunchKernelGGL(attn_combine_few_kernel<128>, fgrid, dim3(HALF_ROWS * 64), 0, s, a);
+    else
+      hipLaunchKernelGGL(attn_combine_few_kernel<64>, fgrid, dim3(HALF_ROWS * 64), 0, s, a);
+    return check_launch("subset_attn combine");
+  }
   if (head_dim == 128)
     hipLaunchKernelGGL(attn_combine_kernel<128>, dim3((unsigned)blocks), dim3(CMB_THREADS), 0, s, a);
   else
