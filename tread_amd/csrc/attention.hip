@@ -43,6 +43,7 @@ constexpr int ATT_NBUF = 3;                    // LDS tile buffers (software pip
 constexpr int N_XCD = 8;
 constexpr int ATT_TARGET_WGS = 512;     // split-K when fewer (head, row tile) work groups than this
 constexpr int ATT_MIN_SPLIT_KEYS = 512;
+constexpr int ATT_MANY_TILE_WGS = 64;   // (head, row tile) work groups from which the split aims higher
 
 struct AttnArgs {
   const bf16_t* q;
@@ -752,7 +753,7 @@ __global__ __launch_bounds__(HALF_ROWS * 64) void attn_halves_kernel(const AttnA
 // weights as attn_combine_kernel (exp2(m_s - M), empty slices skipped). One wave per row instead of
 // a 256-thread work group: a 1.5B-shaped recompute (3 232 rows, 12 / 2 heads, 16 096 keys, 4 slices)
 // measured 321 -> 292 us per attention call, a 0.5B-shaped one (1 632 rows, 6 slices) 108 -> 90 us.
-constexpr int CMB_FEW_SPLITS = 8;
+constexpr int CMB_FEW_SPLITS = 16;
 template <int HD>
 __global__ __launch_bounds__(HALF_ROWS * 64) void attn_combine_few_kernel(const AttnArgs a) {
   constexpr int EPL = HD / 64;  // elements per lane
@@ -819,8 +820,13 @@ static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
   sp.split_len = 0;
   sp.nlong = 0;
   if (base < ATT_TARGET_WGS && t_cap >= 2 * ATT_MIN_SPLIT_KEYS) {
-    int64_t want = (ATT_TARGET_WGS + base - 1) / base;
-    int64_t most = t_cap / ATT_MIN_SPLIT_KEYS;
+    // Launches of many row tiles (ragged key ranges when rows are sorted by position) aim at twice
+    // the work groups in slices of at least twice the keys: a 1.5B-shaped recompute (152 row-tile
+    // groups, 16 096 keys) measured 300 -> 248 us with 7 slices instead of 4; slices of 704 keys
+    // (12 over 8 096) measured slower than 6.
+    const bool many = base >= ATT_MANY_TILE_WGS;
+    int64_t want = ((many ? 2 * ATT_TARGET_WGS : ATT_TARGET_WGS) + base - 1) / base;
+    int64_t most = t_cap / (many ? 2 * ATT_MIN_SPLIT_KEYS : ATT_MIN_SPLIT_KEYS);
     int64_t ns = want < most ? want : most;
     if (ns > CMB_MAX_SPLITS) ns = CMB_MAX_SPLITS;
     if (ns > 1) {
