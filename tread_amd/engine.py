@@ -73,6 +73,7 @@ class _Assembly:
         self.pending = [(b, off, delta) for b, off, delta in sources if getattr(b, "ready", None) is not None]
         self.done = [False] * P.L
         self.table = None
+        self.waited = set()  # ids of copy events the current stream already waits on
         if ready:
             _hip.rope_assemble(ready, K, V, P.inv_freq)
         if not self.pending:
@@ -81,8 +82,14 @@ class _Assembly:
     def ensure(self, l):
         if self.done[l]:
             return
+        # blocks promoted in one batch share their layer-group events: one stream wait per event
+        # (each wait is a barrier packet the GPU processes in order)
+        cur = torch.cuda.current_stream()
         for b, _, _ in self.pending:
-            b.wait([l])
+            e = b.ready[l] if b.ready is not None else None
+            if e is not None and id(e) not in self.waited:
+                cur.wait_event(e)
+                self.waited.add(id(e))
         self.table = _hip.rope_assemble([(b.K, b.V, off, delta) for b, off, delta in self.pending], self.K, self.V,
                                         self.P.inv_freq, layer_lo=l, layer_hi=l + 1, table=self.table)
         self.done[l] = True
