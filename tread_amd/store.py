@@ -83,8 +83,11 @@ class Block:
         if self.ready is None:
             return
         s = stream or torch.cuda.current_stream()
+        seen = set()  # layers of one copy group share its event: one wait each
         for l in (range(len(self.ready)) if layers is None else layers):
-            s.wait_event(self.ready[l])
+            if id(self.ready[l]) not in seen:
+                seen.add(id(self.ready[l]))
+                s.wait_event(self.ready[l])
 
     def synchronize(self):
         """Block the host until every copy of this block is complete (CPU tensors readable)."""
