@@ -29,6 +29,11 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 # WRITE_SIZE x 1.0: the factors a plain copy of known size reads on MI355X); the profiler cannot
 # run inside this process, so the figure is carried here for the workload it was measured on.
 MEASURED_ASSEMBLE_TRAFFIC = {"qwen2.5-7b-32k": 3677613000}
+# HBM bytes per recompute attention call (subset_attn_kernel + attn_halves_kernel), the same two
+# passes and factors on the 6 400-row recompute shape of this workload
+# (`python3 -m tread_amd.kernel_bench attention --shape recompute`): 484.5 + 49.1 MB read,
+# 90.2 + 11.5 MB written
+MEASURED_ATTENTION_TRAFFIC = {"qwen2.5-7b-32k": 635233536}
 # doc blocks the GPU tier holds (with the prefix block); the rest spill to the pinned-host tier
 # and are copied back per request on the store's copy streams (None: everything stays on the GPU)
 GPU_TIER_DOCS = {"qwen2.5-1.5b-16k": 8}
@@ -352,7 +357,8 @@ def main():
             log(f"[bench] recompute attention (selected + query rows): {a_sec * 1e6:.1f} us, {a_tf:.0f} TFLOP/s")
             attn = {"bound": "mfma", "kernel": "tread::subset_attn_kernel (+ attn_halves_kernel)",
                     "achieved": round(a_tf, 1), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(a_tf / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                    "frac": round(a_tf / BF16_MFMA_PEAK_TFLOPS, 4),
+                    "traffic": MEASURED_ATTENTION_TRAFFIC.get(args.workload),
                     "avg_us": round(a_sec * 1e6, 2), "algorithmic_flop": a_flop}
         full_ms = None
         if args.full_reps > 0:
