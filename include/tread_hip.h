@@ -29,14 +29,15 @@ int tread_abi_version(void);
 /* ---------------------------------------------------------------------------------------------
  * (a) Fused RoPE re-rotation + gather/append of cached blocks into one assembled KV cache.
  * Replaces tread/blend.py:22-39 (rotate_keys: K*cos + rotate_half(K)*sin per doc block) and
- * tread/engine.py:233-245 (torch.cat of the prefix and rotated doc blocks along T, then unbind).
+ * tread/engine.py:108-120 (torch.cat of the prefix and rotated doc blocks along T, then unbind).
  * Source i holds K and V as [n_layers, n_kv, n_tokens, head_dim]; its rows land at destination
  * rows [dst_off, dst_off + n_tokens) of dst [n_layers, n_kv, t_cap, head_dim]. K is rotated by
  * `delta` positions: with c, s = cos_sin[i][j] (device fp32 [n_src][head_dim/2][2], the cos and sin
  * of fp32(delta_i) * inv_freq[j] as the reference's rotary embedding computes them), row element j
  * becomes fl(fl(x_j*c) + fl(-x_{j+hd/2}*s)) and element j+hd/2 fl(fl(x_{j+hd/2}*c) + fl(x_j*s)),
  * rounded once to bf16 (the fp32 reference rotation, op for op). delta == 0 and V are bit copies.
- * Only layers [layer_lo, layer_hi) are written.
+ * Only layers [layer_lo, layer_hi) are written. dst_v may be NULL: then only K moves (the sources'
+ * v pointers are ignored), the form of a stand-alone rotate_keys.
  * srcs: HOST array (copied into the kernel arguments; at most 48 sources per internal launch).
  */
 typedef struct tread_src {
@@ -100,7 +101,7 @@ int tread_topk_select_bf16(const void* score, int64_t n, int64_t k, int64_t* sel
  * (c) Selective-recompute attention (MFMA, GQA in-kernel, no mask tensor, no repeat_kv).
  * Replaces tread/blend.py:107-110 (repeat_kv x2 + SDPA with the bool mask arange(T) <= S) and
  * the causal / block-diagonal attention of the query forward and cold prefill
- * (tread/engine.py:206-213,257). Row i of q [n, hq, head_dim] sees cache key j of its KV head
+ * (tread/engine.py:81-88,132). Row i of q [n, hq, head_dim] sees cache key j of its KV head
  * iff j <= kend[i] and (j < n_shared or j >= kseg[i]); kseg may be NULL (then keys [0, kend[i]]).
  * out: [n, hq * head_dim]. scale: softmax scale (head_dim^-0.5). head_dim: 64 or 128.
  * Few rows over a long cache (the query forward) split the key axis across work groups, and a

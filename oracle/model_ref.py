@@ -143,7 +143,7 @@ def forward(m: RefModel, ids, past=None, position_ids=None, mask4d=None):
     """Decoder forward over `ids` (1-D LongTensor) on top of an optional past cache.
 
     Mirrors `model.model(ids[None], past_key_values=..., attention_mask=..., position_ids=...)` as the
-    reference uses it (tread/blend.py:18; tread/engine.py:211-213,257,273,287): positions default to
+    reference uses it (tread/blend.py:18; tread/engine.py:86-88,132,148,162): positions default to
     P..P+n-1 where P is the past length; the mask defaults to causal over the concatenated cache;
     a 4D additive mask [1,1,n,P+n] is used as given. DynamicCache.update concatenates new K/V after
     the past ones (site:transformers/cache_utils.py:113-152).

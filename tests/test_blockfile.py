@@ -133,3 +133,81 @@ def test_scan_skips_foreign_and_partial_files(tmp_path):
     st = BlockStore(1 << 20, 0, disk_dir=tmp_path, disk_budget_bytes=1 << 30)
     assert list(st.disk_blocks) == [key]
     assert sorted(p.name for p in tmp_path.iterdir()) == sorted([key + BF.SUFFIX, "notes.txt"])
+
+
+def _corrupt_payload(path):
+    data = bytearray(path.read_bytes())
+    h = BF.parse_header(bytes(data[:4096]))
+    data[h["k_offset"] + 3] ^= 0x20
+    path.write_bytes(bytes(data))
+
+
+@pytest.mark.parametrize("batched", [False, True])
+def test_corrupt_disk_block_is_a_clean_miss(tmp_path, batched):
+    """A block file whose payload fails its checksum: the lookup misses (the file is dropped and
+    counted), nothing half-read is served or indexed, later lookups of it miss without raising,
+    and the other blocks of the same batch are served exactly."""
+    blocks = {f"{i:064x}": _block(40 + i) for i in range(4)}
+    keys = list(blocks)
+    nb = _nbytes(*blocks[keys[0]])
+    st = BlockStore(nb, 0, disk_dir=tmp_path, disk_budget_bytes=1 << 30)
+    for k, (K, V) in blocks.items():
+        st.put(k, K, V, base=5)
+    st.drain()
+    assert set(st.disk_blocks) == set(keys[:3])
+    _corrupt_payload(tmp_path / (keys[1] + BF.SUFFIX))
+    if batched:
+        with st.batch():
+            st.prefetch(keys[:3])
+            got = [st.get(k) for k in keys[:3]]
+    else:
+        got = [st.get(k) for k in keys[:3]]
+    assert got[1] is None
+    assert st.stats.disk_errors == 1 and st.stats.misses == 1 and st.stats.disk_hits == st.stats.hits == 2
+    assert keys[1] not in st.disk_blocks and keys[1] not in st.blocks
+    assert not (tmp_path / (keys[1] + BF.SUFFIX)).exists()
+    # the GPU tier holds one block: the last good lookup, served exactly
+    b = got[2]
+    assert b is not None and _same(b.K, blocks[keys[2]][0]) and _same(b.V, blocks[keys[2]][1])
+    assert st.get(keys[1]) is None and st.stats.misses == 2 and st.stats.disk_errors == 1
+    # a caller recomputing the block puts it back
+    st.put(keys[1], *blocks[keys[1]], base=5)
+    assert _same(st.get(keys[1]).K, blocks[keys[1]][0])
+
+
+def test_prefetch_keeps_lru_order_and_stats_of_the_lookups(tmp_path):
+    blocks = {f"{i:064x}": _block(50 + i) for i in range(4)}
+    keys = list(blocks)
+    nb = _nbytes(*blocks[keys[0]])
+    st = BlockStore(nb, 0, disk_dir=tmp_path, disk_budget_bytes=1 << 30)
+    for k, (K, V) in blocks.items():
+        st.put(k, K, V, base=1)
+    st.drain()
+    order = list(st.disk_blocks)
+    with st.batch():
+        st.prefetch(keys)
+        assert list(st.disk_blocks) == order and st.stats.disk_hits == 0 and st.stats.hits == 0
+        b = st.get(keys[0])
+    # the lookup moved block 0 to the LRU end; block 3, evicted by its promotion, was spilled after it
+    assert st.stats.disk_hits == 1 and list(st.disk_blocks) == [keys[1], keys[2], keys[0], keys[3]]
+    assert _same(b.K, blocks[keys[0]][0]) and not st._staged  # unconsumed reads are dropped at exit
+
+
+def test_graph_bucket_cache_goes_stale_when_its_bucket_is_claimed():
+    """A cache aliasing a graph bucket raises once a later request claims the bucket; a detached
+    copy stays valid and keeps the rows."""
+    from types import SimpleNamespace
+    from tread_amd.cache import KVCache, StaleCacheError
+    g = SimpleNamespace(generation=3)
+    K = torch.arange(2 * 1 * 2 * 8 * 4, dtype=torch.float32).view(2, 1, 2, 8, 4)
+    V = -K
+    c = KVCache(K, V, 5, graph=g)
+    kept = KVCache(K, V, 5, graph=g).detach()
+    assert c.valid and torch.equal(c.K, K) and len(c.key_cache) == 2
+    g.generation += 1  # the next request claims the bucket
+    assert not c.valid
+    for read in (lambda: c.K, lambda: c.V, lambda: c.key_cache, lambda: c.layers, lambda: c.check()):
+        with pytest.raises(StaleCacheError):
+            read()
+    assert kept.valid and kept.graph is None and kept.K.data_ptr() != K.data_ptr()
+    assert torch.equal(kept.K[..., :5, :], K[..., :5, :]) and torch.equal(kept.V[..., :5, :], V[..., :5, :])

@@ -116,20 +116,28 @@ def delta_table(inv_freq, deltas, device):
 def rope_assemble(sources, dst_k, dst_v, inv_freq, layer_lo=0, layer_hi=None, table=None):
     """sources: list of (K, V, dst_off, delta) with K, V [L, 1, kv, n, hd] bf16 on the GPU.
     dst_k, dst_v: [L, 1, kv, t_cap, hd]. Rotates K by delta (fp32 cos/sin table), copies V.
+    dst_v None moves K only (the sources' V may then be None).
     `table` (from delta_table over the sources' deltas) may be passed to reuse it across calls."""
     _need(dst_k, "dst_k")
-    _need(dst_v, "dst_v")
     L, one, kv, t_cap, hd = dst_k.shape
-    if dst_v.shape != dst_k.shape or one != 1:
-        raise ValueError("dst_k / dst_v must both be [L, 1, kv, t_cap, hd]")
+    if dst_v is not None:
+        _need(dst_v, "dst_v")
+        if dst_v.shape != dst_k.shape:
+            raise ValueError("dst_k / dst_v must both be [L, 1, kv, t_cap, hd]")
+    if one != 1:
+        raise ValueError("dst_k must be [L, 1, kv, t_cap, hd]")
     layer_hi = L if layer_hi is None else layer_hi
     arr = (Src * max(1, len(sources)))()
     for i, (K, V, off, delta) in enumerate(sources):
         _need(K, f"source {i} K")
-        _need(V, f"source {i} V")
-        if K.shape[:3] != (L, 1, kv) or K.shape[-1] != hd or V.shape != K.shape:
+        if K.shape[:3] != (L, 1, kv) or K.shape[-1] != hd:
             raise ValueError(f"source {i}: shape {tuple(K.shape)} does not match cache {tuple(dst_k.shape)}")
-        arr[i] = Src(K.data_ptr(), V.data_ptr(), K.shape[-2], int(off), int(delta))
+        if dst_v is not None:
+            _need(V, f"source {i} V")
+            if V.shape != K.shape:
+                raise ValueError(f"source {i}: V shape {tuple(V.shape)} differs from K {tuple(K.shape)}")
+        vp = V.data_ptr() if dst_v is not None else 0
+        arr[i] = Src(K.data_ptr(), vp, K.shape[-2], int(off), int(delta))
     if table is None:
         table = delta_table(inv_freq, [s[3] for s in sources], dst_k.device)
     if table.shape != (len(sources), hd // 2, 2) or table.dtype != torch.float32 or not table.is_cuda:

@@ -1,9 +1,11 @@
 """KV ops of the reuse path: re-rotation, assembly, deviation scoring and selective recompute.
 
 Public names and signatures follow tread/blend.py (prefill_kv, rotate_keys, chunk_kv, assemble,
-_subset_ctx, _qkv, _layer_subset, layer1_deviation, blend, to_cache) so callers written against
-the reference keep working. KV tensors are [1, kv_heads, T, head_dim] per layer (post-RoPE keys),
-blocks are stacked [L, 1, kv_heads, n, head_dim]. All arithmetic runs in the HIP kernels of
+_subset_ctx, _qkv, _layer_subset, layer1_deviation, blend, to_cache), including the private
+helpers phase0/blend.py re-exports, so callers written against the reference keep working; the
+engine itself runs the fused forms underneath (forward.layer_forward, blend_cache, blend_query).
+KV tensors are [1, kv_heads, T, head_dim] per layer (post-RoPE keys), blocks are stacked
+[L, 1, kv_heads, n, head_dim]. All arithmetic runs in the HIP kernels of
 libtread_hip.so (tread_amd._hip) plus torch GEMMs; bf16 on the GPU only.
 """
 import weakref
@@ -13,7 +15,7 @@ import torch.nn.functional as F
 
 from tread_amd import _hip
 from tread_amd.cache import KVCache
-from tread_amd.forward import alloc_cache, embed, final_logits, make_rows, run_layers, layer_forward
+from tread_amd.forward import Rows, alloc_cache, embed, final_logits, make_rows, run_layers, layer_forward
 from tread_amd.model import prepare
 
 _PREPARED = weakref.WeakKeyDictionary()
@@ -53,16 +55,16 @@ def prefill_kv(model, ids):
 def rotate_keys(model, K, delta):
     """tread/blend.py:22-39: shift post-RoPE keys by `delta` positions, R(p + delta) = R(delta) R(p).
 
-    delta 0 returns K itself. Otherwise one pass of the fused re-rotation kernel with fp32
-    cos/sin and one rounding to bf16 (the fp32-reference result, within 1 bf16 ulp). K: [..., n, hd]
-    with any leading dims (e.g. [L, 1, kv, n, hd])."""
+    delta 0 returns K itself. Otherwise one K-only pass of the fused re-rotation kernel with fp32
+    cos/sin and one rounding to bf16 (the fp32 reference rotation, op for op). K: [..., n, hd] with
+    any leading dims (e.g. [L, 1, kv, n, hd])."""
     if delta == 0:
         return K
     P = prepared(model)
     shape = K.shape
     Kc = K.contiguous().reshape(-1, 1, 1, shape[-2], shape[-1])
     out = torch.empty_like(Kc)
-    _hip.rope_assemble([(Kc, Kc, 0, delta)], out, torch.empty_like(Kc), P.inv_freq)
+    _hip.rope_assemble([(Kc, None, 0, delta)], out, None, P.inv_freq)
     return out.reshape(shape)
 
 
@@ -92,34 +94,88 @@ def assemble(model, prefix_ids, docs_ids, mode):
     return list(K.unbind(0)), list(V.unbind(0))
 
 
-def _subset_ctx(model, S, T, ref=None):
-    """tread/blend.py:71-79: per-blend constants for positions S: RoPE tables (bf16, rounded as
-    the reference's rotary_emb) and the key ends. No mask tensor: the attention kernel evaluates
-    key <= S[i] itself."""
-    return make_rows(prepared(model), S)
+class SubsetCtx(tuple):
+    """What tread/blend.py:71-79 returns, (rope, mask): rope = (cos, sin) [1, n, hd] in the dtype
+    of `ref` (the reference's rotary_emb rounding), mask [1, 1, n, T] bool, key <= S[i]. It also
+    carries `rows`, the per-row RoPE tables and key ends the HIP layer consumes, so a context built
+    once serves every layer of a blend without rebuilding either."""
+
+    def __new__(cls, rope, mask, rows):
+        obj = super().__new__(cls, (rope, mask))
+        obj.rows = rows
+        return obj
 
 
-def _qkv(layer_idx, model, x, rows, K, V):
-    """tread/blend.py:82-90 fused with the splice of tread/blend.py:106: q/k/v GEMM, RoPE, k/v
-    written into cache rows `rows`. Returns q [n, hq, hd]."""
+def _layer_index(model, layer):
+    """Index of `layer` (a decoder layer module of `model`, or an int) in model.model.layers."""
+    if isinstance(layer, int):
+        return layer
+    for i, lyr in enumerate(model.model.layers):
+        if lyr is layer:
+            return i
+    raise ValueError("layer is not a decoder layer of this model")
+
+
+def _rows_of(model, S, ctx=None):
+    """Rows for positions S: from a SubsetCtx, from a (rope, mask) pair built elsewhere (its
+    tables are taken as given; the reference's mask is always key <= S[i]), or built here."""
     P = prepared(model)
-    lw = P.layers[layer_idx]
-    qkv = F.linear(x, lw.wqkv, lw.bqkv)
-    q = torch.empty(x.shape[0], P.hq, P.hd, dtype=x.dtype, device=x.device)
-    _hip.qkv_rope_splice(qkv, rows.cos, rows.sin, rows.rows, P.hq, P.hkv, P.hd, K, V, q_out=q)
-    return q
+    if isinstance(ctx, SubsetCtx):
+        return ctx.rows
+    if ctx is not None:
+        (cos, sin), _ = ctx
+        half = P.hd // 2
+        rows = S.to(torch.int64).contiguous()
+        return Rows(rows=rows, kend=rows, cos=cos.reshape(-1, P.hd)[:, :half].contiguous(),
+                    sin=sin.reshape(-1, P.hd)[:, :half].contiguous())
+    return make_rows(P, S)
 
 
-def _layer_subset(layer_idx, model, h, S, K, V, inplace=False, ctx=None):
-    """tread/blend.py:93-114: recompute decoder layer `layer_idx` for positions S against the full
-    layer cache K, V [1, kv, T, hd]; fresh k/v are spliced at S before attention.
-    h: [1, n, H]. Returns (h, K, V)."""
+def _subset_ctx(model, S, T, ref):
+    """tread/blend.py:71-79: per-blend constants for positions S against a T-row cache: RoPE
+    (cos, sin) [1, n, hd] in ref.dtype and the bool mask arange(T)[None] <= S[:, None] as
+    [1, 1, n, T]. The tables come from the HIP rope-table kernel (the reference's rotary_emb
+    rounding); the attention kernel itself evaluates key <= S[i] and never reads the mask."""
     P = prepared(model)
-    R = ctx if ctx is not None else _subset_ctx(model, S, K.shape[2])
+    R = make_rows(P, S)
+    dt = ref.dtype
+    cos = torch.cat([R.cos, R.cos], dim=-1).to(dt)[None]
+    sin = torch.cat([R.sin, R.sin], dim=-1).to(dt)[None]
+    mask = (torch.arange(T, device=S.device)[None, :] <= S[:, None])[None, None]
+    return SubsetCtx((cos, sin), mask, R)
+
+
+def _qkv(layer, model, x, pos, rope=None):
+    """tread/blend.py:82-90: q/k/v projections of x [1, n, H] (already normed) and RoPE at
+    positions pos. Returns q [1, hq, n, hd], k and v [1, hkv, n, hd] (q and k rotated). `layer` is
+    the decoder layer module (or its index); `rope` an optional (cos, sin) as _subset_ctx gives.
+    One fused q|k|v GEMM, then the HIP RoPE kernel writes rotated q, k and v in head-major order."""
+    P = prepared(model)
+    l = _layer_index(model, layer)
+    lw = P.layers[l]
+    n = x.shape[-2]
+    R = _rows_of(model, pos, None if rope is None else (rope, None))
+    qkv = F.linear(x.reshape(n, P.H), lw.wqkv, lw.bqkv)
+    q = torch.empty(n, P.hq, P.hd, dtype=x.dtype, device=x.device)
+    k = torch.empty(1, P.hkv, n, P.hd, dtype=x.dtype, device=x.device)
+    v = torch.empty_like(k)
+    local = torch.arange(n, device=x.device)
+    _hip.qkv_rope_splice(qkv, R.cos, R.sin, local, P.hq, P.hkv, P.hd, k, v, q_out=q)
+    return q.transpose(0, 1)[None], k, v
+
+
+def _layer_subset(layer, model, h, S, K, V, inplace=False, ctx=None):
+    """tread/blend.py:93-114: recompute decoder layer `layer` (module or index) for positions S
+    against the full layer cache K, V [1, kv, T, hd]; fresh k/v are spliced at S before attention
+    (in place when `inplace`, else into copies). h: [1, n, H]; ctx: _subset_ctx(...), built once
+    per blend. Returns (h, K, V)."""
+    P = prepared(model)
+    l = _layer_index(model, layer)
+    R = _rows_of(model, S, ctx)
     if not inplace:
         K, V = K.clone(), V.clone()
-    Kl, Vl = {layer_idx: K}, {layer_idx: V}
-    h2, d = layer_forward(P, layer_idx, h[0].contiguous(), None, R, Kl, Vl)
+    Kl, Vl = {l: K}, {l: V}
+    h2, d = layer_forward(P, l, h[0].contiguous(), None, R, Kl, Vl)
     return (h2 + d)[None], K, V
 
 
@@ -235,11 +291,30 @@ def _blend(model, ctx_ids, K, V, candidates, ratio, policy, gen, runner, graph, 
 
 
 def blend(model, ctx_ids, K, V, candidates, ratio, policy, gen=None, inplace=False, runner=None):
-    """tread/blend.py:133-179 signature: returns (K list, V list, S, eff)."""
+    """tread/blend.py:133-179 signature: returns (K list, V list, S, eff).
+
+    With a SubsetRunner whose worth_it(T) holds, the recompute layers replay that runner's
+    captured graph: the layers are copied into the bucket's static cache first and back out after
+    (what tread/graphs.py:92-99 does). The engine avoids both copies by assembling straight into
+    the bucket (Engine(graphs=True))."""
     K, V = list(K), list(V)
     if not inplace:
         K, V = [k.clone() for k in K], [v.clone() for v in V]
-    S, eff = blend_cache(model, ctx_ids, K, V, candidates, ratio, policy, gen=gen, runner=None)
+    T = K[0].shape[2] if K else 0
+    n, budget = select(ratio, candidates)
+    if runner is None or not candidates or budget == 0 or not runner.worth_it(T):
+        S, eff = blend_cache(model, ctx_ids, K, V, candidates, ratio, policy, gen=gen)
+        return K, V, S, eff
+    start = 1 if policy == "deviation" else 0
+    g = runner.cache_for(start, budget, T, 0, K[0].device)
+    for l in range(len(K)):
+        g.K[l, :, :, :T].copy_(K[l])
+        g.V[l, :, :, :T].copy_(V[l])
+    S, eff = blend_cache(model, ctx_ids, list(g.Kl), list(g.Vl), candidates, ratio, policy, gen=gen, runner=runner,
+                         graph=g, T=T)
+    for l in range(len(K)):
+        K[l].copy_(g.K[l, :, :, :T])
+        V[l].copy_(g.V[l, :, :, :T])
     return K, V, S, eff
 
 

@@ -75,8 +75,9 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArg
   const int64_t doff = (((int64_t)layer * a.n_kv + head) * a.t_cap + src.dst_off + row0) * HD;
   const int tid = threadIdx.x;
   const int nvec = rows * HD / 8;  // valid 16-byte chunks of this unit's K or V span
-  const u32x4_t* vs = reinterpret_cast<const u32x4_t*>(src.v + soff);
-  u32x4_t* vd = reinterpret_cast<u32x4_t*>(a.dv + doff);
+  const bool has_v = a.dv != nullptr;  // uniform: a K-only launch (rotate_keys) moves no V
+  const u32x4_t* vs = reinterpret_cast<const u32x4_t*>(has_v ? src.v + soff : nullptr);
+  u32x4_t* vd = reinterpret_cast<u32x4_t*>(has_v ? a.dv + doff : nullptr);
 
   if (src.delta == 0) {  // K and V are both bit copies of one contiguous span each
     const u32x4_t* ks = reinterpret_cast<const u32x4_t*>(src.k + soff);
@@ -86,7 +87,7 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArg
     for (int j = 0; j < V_PER_T; ++j) {
       int c = tid + j * ASM_THREADS;
       if (c < nvec) {
-        vb[j] = ldg_nt(vs + c);
+        if (has_v) vb[j] = ldg_nt(vs + c);
         kb[j] = ldg_nt(ks + c);
       }
     }
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArg
     for (int j = 0; j < V_PER_T; ++j) {
       int c = tid + j * ASM_THREADS;
       if (c < nvec) {
-        stg_nt(vd + c, vb[j]);
+        if (has_v) stg_nt(vd + c, vb[j]);
         stg_nt(kd + c, kb[j]);
       }
     }
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArg
 #pragma unroll
   for (int j = 0; j < V_PER_T; ++j) {
     int cc = tid + j * ASM_THREADS;
-    if (cc < nvec) vb[j] = ldg_nt(vs + cc);
+    if (has_v && cc < nvec) vb[j] = ldg_nt(vs + cc);
   }
   if (r < rows) {
     x1 = ldg_nt(reinterpret_cast<const u32x4_t*>(kr + c));
@@ -119,7 +120,7 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArg
 #pragma unroll
   for (int j = 0; j < V_PER_T; ++j) {
     int cc = tid + j * ASM_THREADS;
-    if (cc < nvec) stg_nt(vd + cc, vb[j]);
+    if (has_v && cc < nvec) stg_nt(vd + cc, vb[j]);
   }
   if (r < rows) {
     const float cv[8] = {t0[0], t0[2], t1[0], t1[2], t2[0], t2[2], t3[0], t3[2]};
@@ -154,14 +155,14 @@ extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void
                                         tread_stream_t stream) {
   if (n_src < 0 || (n_src > 0 && !srcs)) return fail(TREAD_EINVAL, "rope_assemble: bad source list");
   if (n_src == 0) return 0;
-  if (!dst_k || !dst_v || !cos_sin) return fail(TREAD_EINVAL, "rope_assemble: null pointer");
+  if (!dst_k || !cos_sin) return fail(TREAD_EINVAL, "rope_assemble: null pointer");
   if (head_dim != 64 && head_dim != 128) return fail(TREAD_EINVAL, "rope_assemble: head_dim %d not in {64,128}", head_dim);
   if (n_kv <= 0 || n_layers <= 0 || t_cap <= 0) return fail(TREAD_EINVAL, "rope_assemble: bad shape");
   if (layer_lo < 0 || layer_hi > n_layers || layer_lo >= layer_hi)
     return fail(TREAD_EINVAL, "rope_assemble: layer range [%d,%d) outside [0,%d)", layer_lo, layer_hi, n_layers);
   for (int i = 0; i < n_src; ++i) {
     const tread_src_t& s = srcs[i];
-    if (!s.k || !s.v) return fail(TREAD_EINVAL, "rope_assemble: source %d has a null pointer", i);
+    if (!s.k || (dst_v && !s.v)) return fail(TREAD_EINVAL, "rope_assemble: source %d has a null pointer", i);
     if (s.n_tokens < 0 || s.dst_off < 0 || s.dst_off + s.n_tokens > t_cap)
       return fail(TREAD_ERANGE, "rope_assemble: source %d rows [%lld,%lld) outside the cache (t_cap %lld)", i,
                   (long long)s.dst_off, (long long)(s.dst_off + s.n_tokens), (long long)t_cap);

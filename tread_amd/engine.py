@@ -117,10 +117,11 @@ class Engine:
         torch.cuda.current_stream().synchronize()
 
     @torch.inference_mode()
-    def prefix_block(self, prefix_ids, st, namespace="", host_ids=None):
+    def prefix_block(self, prefix_ids, st, namespace="", host_ids=None, key=None):
         """tread/engine.py:44-57. `host_ids`: the same ids already in host memory (hashed instead of
-        prefix_ids, which saves a device-to-host copy per key)."""
-        key = block_key(*self.sig, namespace, "prefix", prefix_ids if host_ids is None else host_ids)
+        prefix_ids, which saves a device-to-host copy per key); `key`: the key, if already known."""
+        if key is None:
+            key = block_key(*self.sig, namespace, "prefix", prefix_ids if host_ids is None else host_ids)
         b = self.store.get(key)
         if b is None:
             st.misses += 1
@@ -134,14 +135,16 @@ class Engine:
         return key, b
 
     @torch.inference_mode()
-    def doc_blocks(self, prefix_key, pb, docs, st, host_docs=None):
+    def doc_blocks(self, prefix_key, pb, docs, st, host_docs=None, keys=None):
         """tread/engine.py:59-96: look up every doc; prefill all misses in one packed forward.
 
         The packed sequence sits on top of the prefix rows of a temporary cache; token j of doc i
         has RoPE position P + j, writes cache row P + off_i + j, and sees rows [0, P) plus
         [P + off_i, P + off_i + j]: the reference's block-diagonal mask, evaluated in-kernel.
-        `host_docs`: the docs' ids already in host memory, hashed instead of `docs`."""
-        keys = [block_key(*self.sig, prefix_key, d) for d in (docs if host_docs is None else host_docs)]
+        `host_docs`: the docs' ids already in host memory, hashed instead of `docs`; `keys`: the
+        docs' keys, if already known."""
+        if keys is None:
+            keys = [block_key(*self.sig, prefix_key, d) for d in (docs if host_docs is None else host_docs)]
         blocks = [self.store.get(k) for k in keys]
         miss = [i for i, b in enumerate(blocks) if b is None]
         st.hits += len(docs) - len(miss)
@@ -184,8 +187,11 @@ class Engine:
             hp, *hd = torch.cat([prefix_ids] + list(docs)).to("cpu", torch.int64).split(
                 [len(prefix_ids)] + [len(d) for d in docs])
         with self.store.batch():  # host-tier hits share one layer-major H2D schedule
-            pkey, pb = self.prefix_block(prefix_ids, st, namespace, host_ids=hp)
-            blocks = self.doc_blocks(pkey, pb, docs, st, host_docs=hd)
+            pkey = block_key(*self.sig, namespace, "prefix", prefix_ids if hp is None else hp)
+            dkeys = [block_key(*self.sig, pkey, d) for d in (docs if hd is None else hd)]
+            self.store.prefetch([pkey] + dkeys)  # disk-tier files: read and verified in parallel
+            pkey, pb = self.prefix_block(prefix_ids, st, namespace, host_ids=hp, key=pkey)
+            blocks = self.doc_blocks(pkey, pb, docs, st, host_docs=hd, keys=dkeys)
         Pn = pb.n_tokens
         T = Pn + sum(len(d) for d in docs)
         Nq = len(query_ids)
@@ -247,7 +253,9 @@ class Engine:
         this engine's cache: the token ids' k/v are written in place at rows cache.length.. (no
         per-layer concatenation) and the last one's logits [vocab] are returned. Replayed from a
         graph when the cache is a graph bucket with room for the padded rows; a cache without
-        room grows first. A bucket's cache is valid until the next request replays that bucket."""
+        room grows first. A bucket's cache is valid until the next request claims that bucket
+        (then this raises StaleCacheError; `cache.detach()` keeps a copy that stays valid)."""
+        cache.check()
         n = ids.numel()
         T = cache.length
         if T + n > cache.capacity:

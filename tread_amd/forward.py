@@ -3,9 +3,9 @@
 Every forward on the path is the same computation with different row sets:
   - recompute of positions S (tread/blend.py:93-114): rows = positions = S, keys <= S[i];
   - the deviation pass over all candidates (tread/blend.py:117-130);
-  - the query forward over the assembled cache (tread/engine.py:256-257): rows T..T+Nq-1;
+  - the query forward over the assembled cache (tread/engine.py:131-132): rows T..T+Nq-1;
   - prefix / full prefill (tread/blend.py:12-19; tread/engine.py:155-166): rows 0..N-1;
-  - the packed cold prefill of missed docs (tread/engine.py:200-213): rows after the prefix,
+  - the packed cold prefill of missed docs (tread/engine.py:74-96): rows after the prefix,
     RoPE positions restarting at P per doc, keys = prefix + own doc (block-diagonal).
 A layer is: fused residual-add + RMSNorm (HIP) -> one q|k|v GEMM (hipBLASLt via torch) ->
 RoPE + splice of k/v into the cache (HIP) -> MFMA attention (HIP) -> o_proj GEMM -> fused add +

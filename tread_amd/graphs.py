@@ -11,7 +11,8 @@ rows ride along), where no real row looks, and see no key themselves (key end -1
 the GEMMs their rows but no attention.
 
 Each bucket holds one [L, 1, kv, t_cap, hd] K/V pair; the cache returned by the engine aliases
-it and stays valid until the next request replays the same bucket. The loop is captured as one
+it and stays valid until the next request claims the same bucket (the bucket's generation counter
+then moves on and the old cache raises on access; `KVCache.detach()` keeps a copy). The loop is captured as one
 graph per layer (chained through static hidden-state tensors), so a replay waits for a layer's
 host-tier copies only right before that layer: the block-tier DMAs overlap the recompute.
 """
@@ -91,6 +92,7 @@ class _Graph:
 
     def __init__(self, P, start, nb, Tb, t_cap, device, trim_last, seg=1, nq=0):
         self.t_cap = t_cap
+        self.generation = 0  # bumped whenever a request claims this bucket's cache
         self.queries = {}  # nq -> _QueryGraph over this bucket's cache
         self.K, self.V = alloc_cache(P, t_cap, device)
         self.K.zero_()
@@ -180,6 +182,7 @@ class SubsetRunner:
         forward for n_query rows is captured beside it (before anything is assembled)."""
         nq = _q_bucket(n_query) if (fold and n_query > 0) else 0
         g = self._graph(start, n, T, max(n_query, room or 0), device, nq)
+        g.generation += 1  # a cache handed out for this bucket earlier is about to be overwritten
         if n_query > 0 and not nq:
             nqb = _q_bucket(n_query)
             if nqb not in g.queries:

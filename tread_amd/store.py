@@ -25,8 +25,9 @@ byte budget (LRU): a block leaving the host tier (or leaving the GPU tier when i
 host tier) is written there by a background thread once its D2H has landed, unless its file
 already exists; blocks are immutable and content-addressed, so the disk tier is inclusive (a file
 stays after its block is promoted) and a file is written once. A lookup that misses the GPU and
-host tiers reads the file straight into pinned buffers (inside `batch()`, reads of several blocks
-run in parallel and the H2D schedule waits for them) and promotes the block like a host-tier hit.
+host tiers reads the file straight into pinned buffers, verifies its checksums and promotes the
+block like a host-tier hit (`prefetch()` reads a request's files in parallel first); a file that
+fails to read or verify is deleted and the lookup is a miss, so the block is computed again.
 A new store on the same directory indexes the files found there, so cached blocks survive restarts.
 The store is single-threaded (callers serialise requests), as in the reference; only file I/O runs
 on helper threads.
@@ -123,6 +124,7 @@ class StoreStats:
     spills: int = 0  # block files written
     disk_evictions: int = 0  # block files deleted for the disk budget
     disk_bytes_used: int = 0
+    disk_errors: int = 0  # block files that failed to read or verify (dropped; the lookup missed)
 
 
 class _DiskEntry:
@@ -149,7 +151,7 @@ class BlockStore:
         self.disk_budget = disk_budget_bytes if disk_dir is not None else 0
         self.disk_blocks: "OrderedDict[str, _DiskEntry]" = OrderedDict()
         self._writer = self._readers = None
-        self._reads = []  # (future, Block) of disk reads the pending H2D schedule waits for
+        self._staged = {}  # key -> host Block read and verified by prefetch(), not yet looked up
         self._device = torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() \
             else torch.device("cpu")
         if self.disk_dir is not None:
@@ -164,8 +166,18 @@ class BlockStore:
         self._d2h = []  # (GPU Block, host Block): evictions whose DMAs are not queued yet
 
     def _reap(self):
+        """Drop the references of DMAs that have landed; a promoted block whose last layer group
+        has landed stops being pending (consumers then take it as resident, no event wait)."""
         if self._inflight:
-            self._inflight = [(e, refs) for e, refs in self._inflight if not e.query()]
+            keep = []
+            for e, refs, blocks in self._inflight:
+                if e.query():
+                    for b in blocks:
+                        if b.ready is not None and b.ready and b.ready[-1] is e:
+                            b.ready = None
+                else:
+                    keep.append((e, refs, blocks))
+            self._inflight = keep
 
     # ---- copy engine
     def _stream(self, kind, device):
@@ -188,15 +200,12 @@ class BlockStore:
         finally:
             self._batch -= 1
             if self._batch == 0:
+                self._staged.clear()
                 self.flush()
 
     def flush(self):
         """Queue the pending DMAs: promotions layer-major on the H2D stream, then evictions on the
         D2H stream."""
-        if self._reads:
-            reads, self._reads = self._reads, []
-            for fut, _ in reads:
-                fut.result()  # the file's bytes are in the pinned buffers (or its error raises)
         if self._h2d:
             pend, self._h2d = self._h2d, []
             dev = pend[0][0].K.device
@@ -216,7 +225,8 @@ class BlockStore:
                 b.K.record_stream(s)
                 b.V.record_stream(s)
                 b.ready = events
-            self._inflight.append((events[-1], tuple(t for _, hK, hV in pend for t in (hK, hV))))
+            self._inflight.append((events[-1], tuple(t for _, hK, hV in pend for t in (hK, hV)),
+                                   tuple(b for b, _, _ in pend)))
         if self._d2h:
             pend, self._d2h = self._d2h, []
             for gb, hb in pend:
@@ -236,7 +246,7 @@ class BlockStore:
         gb.V.record_stream(s)
         hb.host_ready = e
         hb.K._tread_ready = e
-        self._inflight.append((e, (hb.K, hb.V)))
+        self._inflight.append((e, (hb.K, hb.V), ()))
 
     def _to_device(self, b: Block):
         """Promote a host-tier block: GPU tensors now, its DMAs with the batch's schedule."""
@@ -402,28 +412,78 @@ class BlockStore:
             self.flush()  # queue its D2H so that the writer can wait for it
 
     def _from_disk(self, key):
+        """The disk-tier block of `key` as a host Block (its bytes verified), or None: not in the
+        tier, or its file failed to read or verify (then the file is dropped and counted in
+        stats.disk_errors, and the lookup is a miss, so the caller recomputes the block)."""
         e = self.disk_blocks.get(key)
         if e is None:
             return None
-        self.disk_blocks.move_to_end(key)
+        staged = self._staged.pop(key, None)
+        if staged is not None:  # read and verified by prefetch()
+            self.disk_blocks.move_to_end(key)
+            return staged
         e.settle()
-        h = e.header
-        nbytes = 2 * int(torch.Size(h["shape"]).numel()) * torch.empty((), dtype=h["dtype"]).element_size()
         if e.block is not None:  # still being written: serve the host copy the writer reads
+            self.disk_blocks.move_to_end(key)
             src = e.block
             return Block(K=src.K, V=src.V, base=src.base, n_tokens=src.n_tokens, nbytes=src.nbytes,
                          device=self._device, host_ready=src.host_ready)
+        b = self._read_file(e)
+        if b is None:
+            self._drop_corrupt(key)
+            return None
+        self.disk_blocks.move_to_end(key)
+        return b
+
+    def _read_file(self, e):
+        """Read a block file into new (pinned) host buffers; None if it cannot be read or verified."""
+        h = e.header
+        nbytes = 2 * int(torch.Size(h["shape"]).numel()) * torch.empty((), dtype=h["dtype"]).element_size()
         pin = self._device.type == "cuda"
         K = torch.empty(h["shape"], dtype=h["dtype"], pin_memory=pin)
         V = torch.empty(h["shape"], dtype=h["dtype"], pin_memory=pin)
-        b = Block(K=K, V=V, base=h["base"], n_tokens=h["n_tokens"], nbytes=nbytes, device=self._device)
-        if self._batch > 0 and pin:
+        try:
+            blockfile.read_into(e.path, K, V)
+        except (OSError, ValueError):  # BlockFileError is a ValueError
+            return None
+        return Block(K=K, V=V, base=h["base"], n_tokens=h["n_tokens"], nbytes=nbytes, device=self._device)
+
+    def _drop_corrupt(self, key):
+        e = self.disk_blocks.pop(key)
+        e.path.unlink(missing_ok=True)
+        self.stats.disk_bytes_used -= e.header["file_bytes"]
+        self.stats.disk_errors += 1
+
+    def prefetch(self, keys):
+        """Read the disk-tier blocks among `keys` (those in neither the GPU nor the host tier) in
+        parallel and verify them, before they are looked up: the lookups inside this batch() then
+        take them from memory, and a file that fails to read or verify is dropped first, so its
+        lookup is a clean miss. LRU order and statistics are those of the lookups alone."""
+        if self.disk_dir is None or self._batch == 0:
+            return
+        todo = []
+        for k in keys:
+            if k in self.blocks or k in self.cpu_blocks or k in self._staged:
+                continue
+            e = self.disk_blocks.get(k)
+            if e is None:
+                continue
+            e.settle()
+            if e.block is None:
+                todo.append((k, e))
+        if not todo:
+            return
+        if len(todo) == 1:
+            results = [self._read_file(todo[0][1])]
+        else:
             if self._readers is None:
                 self._readers = ThreadPoolExecutor(min(8, os.cpu_count() or 1), thread_name_prefix="tread-read")
-            self._reads.append((self._readers.submit(blockfile.read_into, e.path, K, V, None), b))
-        else:
-            blockfile.read_into(e.path, K, V)
-        return b
+            results = list(self._readers.map(lambda ke: self._read_file(ke[1]), todo))
+        for (k, _), b in zip(todo, results):
+            if b is None:
+                self._drop_corrupt(k)
+            else:
+                self._staged[k] = b
 
     def persist(self):
         """Give every block of the GPU and host tiers that has no file yet one (within the disk
