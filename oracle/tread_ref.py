@@ -133,24 +133,32 @@ def prefill_kv(m, ids):
     return K, V
 
 
+def _delta_cos_sin(m, delta, dtype):
+    """cos/sin of the one position `delta` as [1, hd], broadcast over a block's rows. The reference
+    builds rotary_emb(K, full((1, n), delta)), n identical rows (tread/blend.py:34-36); computing
+    the row once keeps every row's fp32 cos/sin identical, as they are in the reference, where
+    torch's CPU threading would otherwise split a large [n, hd] table into chunks whose ragged
+    tails go through a second cos/sin routine."""
+    cos, sin = M.rope_cos_sin(m, torch.full((1,), delta, dtype=torch.long), dtype)
+    return cos[0], sin[0]
+
+
 def rotate_keys(m, K, delta):
     """tread/blend.py:22-39: delta 0 returns K itself; otherwise cos/sin of delta in K.dtype and
     K*cos + rotate_half(K)*sin (attention_scaling is 1 for default RoPE)."""
     if delta == 0:
         return K
-    n = K.shape[-2]
-    cos, sin = M.rope_cos_sin(m, torch.full((n,), delta, dtype=torch.long), K.dtype)
-    return K * cos[0] + M.rotate_half(K) * sin[0]
+    cos, sin = _delta_cos_sin(m, delta, K.dtype)
+    return K * cos + M.rotate_half(K) * sin
 
 
 def rotate_keys_fp32(m, K, delta):
     """The fp32 reference for a re-rotation: fp32 K, unrounded fp32 cos/sin, one rounding to K.dtype."""
     if delta == 0:
         return K.clone()
-    n = K.shape[-2]
-    cos, sin = M.rope_cos_sin(m, torch.full((n,), delta, dtype=torch.long), torch.float32)
+    cos, sin = _delta_cos_sin(m, delta, torch.float32)
     K32 = K.float()
-    return (K32 * cos[0] + M.rotate_half(K32) * sin[0]).to(K.dtype)
+    return (K32 * cos + M.rotate_half(K32) * sin).to(K.dtype)
 
 
 def chunk_kv(m, prefix_ids, doc_ids, mode):

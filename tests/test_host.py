@@ -154,3 +154,28 @@ def test_tier_move_layer_groups_tile_the_layers(L):
     widths = [b - a for a, b in g]
     assert all(widths[i] <= widths[i + 1] for i in range(len(widths) - 2))  # the last may be cut short
     assert widths[0] <= 2
+
+
+def test_rotation_table_equals_the_oracle_cos_sin_and_float64():
+    """The fp32 (cos, sin) table kernel (a) rotates with is the oracle's fp32 cos/sin of the same
+    delta bit for bit (so the kernel's rotation can be compared bit-exactly), and within one fp32
+    ulp of the float64 values of the same fp32 angle."""
+    import math
+    from oracle import model_ref as M
+    from oracle import tread_ref as R
+    from tread_amd import _hip
+    from tread_amd.model import preset
+    for name in ("qwen2.5-7b", "qwen2.5-0.5b", "llama3-70b"):
+        cfg = preset(name)
+        m = M.RefModel(cfg=cfg, w={}, dtype=torch.float32, inv_freq=M.inv_freq_of(cfg))
+        deltas = [0, 1, -1, 7, 999, 1000, -31000, 31000, 12345, 32064, -2**20]
+        tab = _hip.delta_table_host(m.inv_freq, deltas)
+        half = cfg.head_dim // 2
+        for i, d in enumerate(deltas):
+            c, s = R._delta_cos_sin(m, d, torch.float32)
+            assert torch.equal(tab[i, :, 0], c[0, :half]) and torch.equal(tab[i, :, 1], s[0, :half]), (name, d)
+            ang = (m.inv_freq * float(d)).double()  # the fp32 angle, exactly
+            for j in range(half):
+                for v, ref in ((tab[i, j, 0].item(), math.cos(ang[j].item())), (tab[i, j, 1].item(), math.sin(ang[j].item()))):
+                    ulp = 2.0 ** (math.floor(math.log2(abs(ref))) - 23) if ref != 0 else 2 ** -149  # fp32 ulp
+                    assert abs(v - ref) <= max(ulp, 2 ** -126), (name, d, j, v, ref)

@@ -104,13 +104,17 @@ def _freq(inv_freq):
 
 # ------------------------------------------------------------------------------------------- (a)
 
-def delta_table(inv_freq, deltas, device):
-    """fp32 [n, hd/2, 2] (cos, sin) of fp32(delta) * inv_freq, computed with the same torch ops as
-    the reference's rotary embedding (fp32 outer product, then cos / sin), moved to `device`."""
+def delta_table_host(inv_freq, deltas):
+    """fp32 [n, hd/2, 2] (cos, sin) of fp32(delta) * inv_freq on the host, computed with the same
+    torch ops as the reference's rotary embedding (fp32 outer product, then cos / sin)."""
     pos = torch.tensor([int(d) for d in deltas], dtype=torch.int64)
     freqs = (inv_freq.detach().to("cpu", torch.float32)[:, None] @ pos[None, :].float()).transpose(0, 1)
-    tab = torch.stack([freqs.cos(), freqs.sin()], dim=-1).contiguous()
-    return tab.pin_memory().to(device, non_blocking=True)
+    return torch.stack([freqs.cos(), freqs.sin()], dim=-1).contiguous()
+
+
+def delta_table(inv_freq, deltas, device):
+    """delta_table_host, moved to `device`."""
+    return delta_table_host(inv_freq, deltas).pin_memory().to(device, non_blocking=True)
 
 
 def rope_assemble(sources, dst_k, dst_v, inv_freq, layer_lo=0, layer_hi=None, table=None):

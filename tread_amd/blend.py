@@ -306,15 +306,17 @@ def blend(model, ctx_ids, K, V, candidates, ratio, policy, gen=None, inplace=Fal
         S, eff = blend_cache(model, ctx_ids, K, V, candidates, ratio, policy, gen=gen)
         return K, V, S, eff
     start = 1 if policy == "deviation" else 0
-    g = runner.cache_for(start, budget, T, 0, K[0].device)
-    for l in range(len(K)):
-        g.K[l, :, :, :T].copy_(K[l])
-        g.V[l, :, :, :T].copy_(V[l])
-    S, eff = blend_cache(model, ctx_ids, list(g.Kl), list(g.Vl), candidates, ratio, policy, gen=gen, runner=runner,
-                         graph=g, T=T)
-    for l in range(len(K)):
-        K[l].copy_(g.K[l, :, :, :T])
-        V[l].copy_(g.V[l, :, :, :T])
+    with torch.inference_mode():  # the bucket's buffers are inference tensors; K, V stay the caller's kind
+        g = runner.cache_for(start, budget, T, 0, K[0].device)
+        for l in range(len(K)):
+            g.K[l, :, :, :T].copy_(K[l])
+            g.V[l, :, :, :T].copy_(V[l])
+        S, eff = blend_cache(model, ctx_ids, list(g.Kl), list(g.Vl), candidates, ratio, policy, gen=gen,
+                             runner=runner, graph=g, T=T)
+        for l in range(len(K)):
+            K[l].copy_(g.K[l, :, :, :T])
+            V[l].copy_(g.V[l, :, :, :T])
+        S = S.clone()
     return K, V, S, eff
 
 
