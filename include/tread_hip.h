@@ -23,7 +23,7 @@ typedef void* tread_event_t;  /* hipEvent_t */
 
 /* Thread-local text of the last error (empty string if none). */
 const char* tread_last_error(void);
-/* ABI version of this header (7); bumps on any signature change. */
+/* ABI version of this header (8); bumps on any signature change. */
 int tread_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------
@@ -114,6 +114,21 @@ size_t tread_subset_attn_workspace_bytes(int64_t n, int hq, int hkv, int head_di
 int tread_subset_attn_bf16(const void* q, const void* k_cache, const void* v_cache, const int64_t* kend,
                            const int64_t* kseg, int64_t n_shared, int64_t n, int hq, int hkv, int head_dim,
                            int64_t t_cap, float scale, void* out, void* ws, size_t ws_bytes, tread_stream_t stream);
+
+/* tread_subset_attn_bf16 without the workspace argument, for callers that cannot allocate device
+ * memory (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. It calls no allocator: the key-split / key-half partials live in a
+ * static device array of TREAD_SUBSET_ATTN_SCRATCH_BYTES (128 MiB) that each GPU the library runs
+ * on holds until the process ends; its address is looked up on the first call on each device. A
+ * shape whose workspace (tread_subset_attn_workspace_bytes) exceeds that size returns TREAD_ERANGE
+ * with a message and launches nothing. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, two threads) race. Same kernels and results as the workspace
+ * form with a large enough workspace.
+ */
+#define TREAD_SUBSET_ATTN_SCRATCH_BYTES (128u << 20)
+int tread_subset_attn_scratch_bf16(const void* q, const void* k_cache, const void* v_cache, const int64_t* kend,
+                                   const int64_t* kseg, int64_t n_shared, int64_t n, int hq, int hkv, int head_dim,
+                                   int64_t t_cap, float scale, void* out, tread_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Decoder-layer glue for the recompute rows (transformers Qwen2RMSNorm / Qwen2MLP as called at

@@ -10,7 +10,7 @@ from pathlib import Path
 import torch  # loads torch's HIP runtime first, so the library below binds to the same one
 
 LIB_PATH = Path(__file__).resolve().with_name("libtread_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 c_i64, c_int, c_void, c_float, c_size = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
 P_I64 = ctypes.POINTER(ctypes.c_int64)
@@ -37,6 +37,8 @@ _SIGS = {
     "tread_subset_attn_workspace_bytes": (c_size, [c_i64, c_int, c_int, c_int, c_i64]),
     "tread_subset_attn_bf16": (c_int, [c_void, c_void, c_void, c_void, c_void, c_i64, c_i64, c_int, c_int, c_int,
                                        c_i64, c_float, c_void, c_void, c_size, c_void]),
+    "tread_subset_attn_scratch_bf16": (c_int, [c_void, c_void, c_void, c_void, c_void, c_i64, c_i64, c_int, c_int,
+                                               c_int, c_i64, c_float, c_void, c_void]),
     "tread_add_rmsnorm_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_int, c_void, c_void, c_void]),
     "tread_silu_mul_bf16": (c_int, [c_void, c_i64, c_int, c_void, c_void]),
     "tread_skinny_workspace_bytes": (c_size, [c_i64, c_i64, c_i64]),
@@ -351,6 +353,30 @@ def subset_attn(q, k_cache, v_cache, kend, hq, hkv, hd, scale, kseg=None, n_shar
     _check("tread_subset_attn_bf16", lib().tread_subset_attn_bf16(
         _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(kend), _ptr(kseg), int(n_shared), n, hq, hkv, hd,
         t_cap, float(scale), _ptr(out), _ptr(ws), wsb, _stream()))
+    return out
+
+
+SUBSET_ATTN_SCRATCH_BYTES = 128 << 20  # TREAD_SUBSET_ATTN_SCRATCH_BYTES
+
+
+def subset_attn_scratch(q, k_cache, v_cache, kend, hq, hkv, hd, scale, out, kseg=None, n_shared=0):
+    """subset_attn through the entry point that allocates nothing: its partials live in the
+    library's static per-device scratch array (shared by every call on the GPU: calls that overlap
+    on one GPU race). The caller passes `out` [n, hq*hd]. Shapes whose workspace exceeds
+    SUBSET_ATTN_SCRATCH_BYTES raise."""
+    _need(q, "q")
+    _need(k_cache, "k_cache")
+    _need(v_cache, "v_cache")
+    _need(kend, "kend", torch.int64)
+    _need(out, "out")
+    if kseg is not None:
+        _need(kseg, "kseg", torch.int64)
+    n = kend.numel()
+    if q.numel() != n * hq * hd or out.numel() != n * hq * hd:
+        raise ValueError(f"q / out must hold {n}x{hq}x{hd} elements")
+    _check("tread_subset_attn_scratch_bf16", lib().tread_subset_attn_scratch_bf16(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(kend), _ptr(kseg), int(n_shared), n, hq, hkv, hd,
+        k_cache.shape[-2], float(scale), _ptr(out), _stream()))
     return out
 
 

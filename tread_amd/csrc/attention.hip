@@ -30,6 +30,8 @@
 // its running (max, sum) to a workspace, and a combine kernel merges the splits per row.
 #include <utility>
 
+#include <mutex>
+
 #include "common.h"
 #include "../../include/tread_hip.h"
 
@@ -854,6 +856,10 @@ static size_t split_ws_bytes(const SplitPlan& sp, int hkv, int head_dim) {
 
 using namespace tread;
 
+static int subset_attn_impl(const void* q, const void* k_cache, const void* v_cache, const int64_t* kend,
+                            const int64_t* kseg, int64_t n_shared, int64_t n, int hq, int hkv, int head_dim,
+                            int64_t t_cap, float scale, void* out, void* ws, size_t ws_bytes, tread_stream_t stream);
+
 extern "C" size_t tread_subset_attn_workspace_bytes(int64_t n, int hq, int hkv, int head_dim, int64_t t_cap) {
   if (n <= 0 || hq <= 0 || hkv <= 0 || (hq % hkv) != 0 || t_cap <= 0) return 0;
   return split_ws_bytes(plan_split(n, hq, hkv, t_cap), hkv, head_dim);
@@ -863,6 +869,71 @@ extern "C" int tread_subset_attn_bf16(const void* q, const void* k_cache, const 
                                       const int64_t* kseg, int64_t n_shared, int64_t n, int hq, int hkv, int head_dim,
                                       int64_t t_cap, float scale, void* out, void* ws, size_t ws_bytes,
                                       tread_stream_t stream) {
+  return subset_attn_impl(q, k_cache, v_cache, kend, kseg, n_shared, n, hq, hkv, head_dim, t_cap, scale, out, ws,
+                          ws_bytes, stream);
+}
+
+// ---- the same attention with its fp32 partials in a static per-device scratch array -------------
+// For callers that cannot allocate (graph capture, serving loops): the key-split and key-half
+// partials live in `scratch`, a file-scope device array of TREAD_SUBSET_ATTN_SCRATCH_BYTES that each
+// GPU the library runs on holds until the process ends. Host code never passes the array's name to
+// a kernel (on the host it is only a stand-in): its device address is looked up once per device
+// with hipGetSymbolAddress and kept in g_scratch_ptr. Every call on one GPU shares that GPU's
+// array, so calls that overlap on one GPU race; nothing in it has to start at zero (every partial
+// the merge kernels read is written by the attention kernel of the same call).
+static __device__ __align__(256) unsigned char scratch[TREAD_SUBSET_ATTN_SCRATCH_BYTES];
+
+namespace {
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[SCRATCH_MAX_DEVICES];
+}  // namespace
+
+// The current device's address of `scratch`, looked up on the first call on that device.
+static int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail((int)e, "subset_attn_scratch: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= SCRATCH_MAX_DEVICES)
+    return fail(TREAD_ERANGE, "subset_attn_scratch: device %d outside the %d supported", dev, SCRATCH_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(e != hipSuccess ? (int)e : TREAD_EINVAL, "subset_attn_scratch: hipGetSymbolAddress: %s",
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+extern "C" int tread_subset_attn_scratch_bf16(const void* q, const void* k_cache, const void* v_cache,
+                                              const int64_t* kend, const int64_t* kseg, int64_t n_shared, int64_t n,
+                                              int hq, int hkv, int head_dim, int64_t t_cap, float scale, void* out,
+                                              tread_stream_t stream) {
+  if (n == 0) return 0;
+  if (n < 0 || hq <= 0 || hkv <= 0 || (hq % hkv) != 0 || t_cap <= 0)
+    return fail(TREAD_EINVAL, "subset_attn_scratch: bad shape (n=%lld hq=%d hkv=%d)", (long long)n, hq, hkv);
+  const size_t need = split_ws_bytes(plan_split(n, hq, hkv, t_cap), hkv, head_dim);
+  if (need > (size_t)TREAD_SUBSET_ATTN_SCRATCH_BYTES)
+    return fail(TREAD_ERANGE,
+                "subset_attn_scratch: this shape (n=%lld hq=%d hkv=%d head_dim=%d t_cap=%lld) needs %zu bytes of "
+                "scratch, above the static maximum of %zu; call tread_subset_attn_bf16 with a workspace instead",
+                (long long)n, hq, hkv, head_dim, (long long)t_cap, need, (size_t)TREAD_SUBSET_ATTN_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need) {
+    int rc = scratch_for_current_device(&ws);
+    if (rc) return rc;
+  }
+  return subset_attn_impl(q, k_cache, v_cache, kend, kseg, n_shared, n, hq, hkv, head_dim, t_cap, scale, out, ws,
+                          need ? (size_t)TREAD_SUBSET_ATTN_SCRATCH_BYTES : 0, stream);
+}
+
+static int subset_attn_impl(const void* q, const void* k_cache, const void* v_cache, const int64_t* kend,
+                            const int64_t* kseg, int64_t n_shared, int64_t n, int hq, int hkv, int head_dim,
+                            int64_t t_cap, float scale, void* out, void* ws, size_t ws_bytes, tread_stream_t stream) {
   if (n == 0) return 0;
   if (n < 0 || hq <= 0 || hkv <= 0 || (hq % hkv) != 0 || t_cap <= 0)
     return fail(TREAD_EINVAL, "subset_attn: bad shape (n=%lld hq=%d hkv=%d)", (long long)n, hq, hkv);
