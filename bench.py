@@ -168,13 +168,62 @@ def time_decode(eng, system, docs, query, ratio, n):
             "graph": cache.graph is not None}
 
 
+def ratio_sweep(eng, system, order, query, ratios, steps, full_ms, full_logits, headline):
+    """The reference's ratio sweep (bench/bench_scaling.py:68-72,88-91) on the timed request: for
+    each recompute ratio, the median TTFT of `steps` warm requests (after one untimed request that
+    captures the ratio's graph bucket), the speedup over full prefill, and the first-token KL and
+    top-1 agreement against full prefill's logits. The headline ratio reuses its timed requests."""
+    import torch.nn.functional as F
+    out = []
+    for r in ratios:
+        if r == headline[0]:
+            t = list(headline[1])
+            logits, _, st = eng.prefill(system, order, query, ratio=r)
+        else:
+            eng.prefill(system, order, query, ratio=r)
+            t = []
+            for _ in range(steps):
+                logits, _, st = eng.prefill(system, order, query, ratio=r)
+                t.append(st.t["ttft"])
+        ms = statistics.median(t) * 1e3
+        row = {"ratio": r, "ttft_ms": round(ms, 2), "recompute_eff": round(st.recompute_eff, 4),
+               "stages_ms": {k: round(v * 1e3, 2) for k, v in st.t.items()}}
+        if full_logits is not None:
+            a, b = full_logits.float(), logits.float()
+            kl = F.kl_div(F.log_softmax(b, -1), F.log_softmax(a, -1), log_target=True, reduction="sum").item()
+            row.update(speedup_vs_full_prefill=round(full_ms / ms, 2), kl_vs_full_prefill=float(f"{kl:.4g}"),
+                       top1_matches_full_prefill=bool(int(a.argmax()) == int(b.argmax())))
+        log(f"[bench] sweep r={r}: ttft {ms:.1f} ms" + (f", {row['speedup_vs_full_prefill']}x, KL {row['kl_vs_full_prefill']}, "
+                                                        f"top-1 {'=' if row['top1_matches_full_prefill'] else '!='}"
+                                                        if full_logits is not None else ""))
+        out.append(row)
+    return out
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(preset_name, n_docs, doc_len, n_sys, n_query, ratio, threads):
-    """The oracle (the reference's torch path restated on the CPU, bf16) timed on a bounded sample
-    of the same workload and extrapolated to one request's TTFT:
-      assemble: rotate_keys + cat of 4 doc blocks (of n_docs), x n_docs/4;
-      deviation: layer 0 + layer-1 k/v + score for 1% of the candidates over the full cache, x100;
-      recompute: one layer for 10% of the selected rows over the full cache, x10 x (L - 1);
-      query: one layer for the query rows, x L."""
+    """The oracle (the reference's torch path restated on the CPU, bf16) timed on this machine's
+    host cores, stage by stage on the request's own sizes:
+      assemble: rotate_keys of every doc block by its shift + the per-layer cat (tread/engine.py:
+        108-120), all n_docs blocks, in full;
+      deviation: layer 0 over every candidate, layer-1 k/v, the score and the top-k
+        (tread/blend.py:117-130,160), in full (attention in row chunks to bound memory);
+      recompute: one recompute layer over all selected rows against the full cache, x (L - 1)
+        (extrapolated: every recompute layer does the same work);
+      query: one layer of the query forward over the blended cache, x L (extrapolated).
+    Assemble and the two extrapolated layers are timed on their second run (the first builds the
+    CPU kernels' primitives); the deviation pass, ~10 s, runs once.
+    Random N(0, 0.02) weights for the two layers it runs; the embedding lookup (a gather) is not
+    timed."""
     from oracle import model_ref as M
     from oracle import tread_ref as R
     from tread_amd.model import preset
@@ -199,55 +248,68 @@ def cpu_baseline(preset_name, n_docs, doc_len, n_sys, n_query, ratio, threads):
         w[pre + "input_layernorm.weight"] = torch.ones(H, dtype=dt)
         w[pre + "post_attention_layernorm.weight"] = torch.ones(H, dtype=dt)
     m = M.RefModel(cfg=cfg, w=w, dtype=dt, inv_freq=M.inv_freq_of(cfg))
-    Kc = torch.randn(1, hkv, T + n_query, hd, generator=g).to(dt)
-    Vc = torch.randn(1, hkv, T + n_query, hd, generator=g).to(dt)
+    mk = lambda n: torch.randn(1, hkv, n, hd, generator=g).to(dt)
     parts = {}
-    # assemble sample
-    blocks = [(torch.randn(L, 1, hkv, doc_len, hd, generator=g).to(dt), torch.randn(L, 1, hkv, doc_len, hd, generator=g).to(dt))
-              for _ in range(4)]
+    # assemble: every doc block (four distinct random blocks, cycled; the work does not depend on
+    # the values), rotated by its shift, then one cat per layer
+    blocks = [(torch.randn(L, 1, hkv, doc_len, hd, generator=g).to(dt),
+               torch.randn(L, 1, hkv, doc_len, hd, generator=g).to(dt)) for _ in range(4)]
     pref = (torch.randn(L, 1, hkv, n_sys, hd, generator=g).to(dt),) * 2
-    t0 = time.perf_counter()
-    Ks, Vs, off = [pref[0]], [pref[1]], n_sys
-    for K, V in blocks:
-        Ks.append(R.rotate_keys(m, K, off + 7 * doc_len - n_sys))
-        Vs.append(V)
-        off += doc_len
-    torch.cat(Ks, dim=-2).unbind(0), torch.cat(Vs, dim=-2).unbind(0)
-    parts["assemble"] = (time.perf_counter() - t0) * n_docs / 4
-    # deviation sample: layer 0 for 1% of candidates, layer-1 k/v, score
+    perm = torch.randperm(n_docs, generator=g).tolist()
+    for _ in range(2):  # the second run is timed (the first creates the kernels' primitives)
+        t0 = time.perf_counter()
+        Ks, Vs, off = [pref[0]], [pref[1]], n_sys
+        for slot in range(n_docs):
+            K, V = blocks[slot % 4]
+            Ks.append(R.rotate_keys(m, K, off - (n_sys + perm[slot] * doc_len)))
+            Vs.append(V)
+            off += doc_len
+        Kl = list(torch.cat(Ks, dim=-2).unbind(0))
+        Vl = list(torch.cat(Vs, dim=-2).unbind(0))
+        parts["assemble"] = time.perf_counter() - t0
+        del Ks, Vs
+    del blocks
+    K0, V0 = Kl[0].clone(), Vl[0].clone()
+    K1, V1 = Kl[1].clone(), Vl[1].clone()
+    del Kl, Vl
+    # deviation pass over every candidate, then the top-k
     n = n_docs * doc_len
-    nd = max(1, n // 100)
-    all_c = torch.sort(torch.randperm(n, generator=g)[:nd]).values + n_sys
-    h0 = torch.randn(1, nd, H, generator=g).to(dt) * 0.02
+    all_c = torch.arange(n_sys, T)
+    h0 = (torch.randn(1, n, H, generator=g) * 0.02).to(dt)
+    budget = int(round(ratio * n))
     t0 = time.perf_counter()
     ctx = R.subset_ctx(m, all_c, T, dt)
-    Kt, Vt = Kc[:, :, :T], Vc[:, :, :T]  # the blend runs on the T-row context cache
-    h, _, _ = R.layer_subset(m, 0, h0, all_c, Kt, Vt, inplace=True, ctx=ctx)
+    h, _, _ = R.layer_subset_rows(m, 0, h0, all_c, K0, V0, ctx)
     _, k1, v1 = M.qkv(m, 1, M.norm(m, "model.layers.1.input_layernorm", h), *ctx[0])
-    dev = R.deviation_score(k1, v1, Kt[:, :, all_c], Vt[:, :, all_c])[0]
-    dev.topk(max(1, int(round(ratio * nd))))
-    parts["deviation"] = (time.perf_counter() - t0) * n / nd
-    # recompute sample: one layer for 10% of the selected rows
-    nS = int(round(ratio * n))
-    ns = max(1, nS // 10)
-    S = torch.sort(torch.randperm(n, generator=g)[:ns]).values + n_sys
-    hs = torch.randn(1, ns, H, generator=g).to(dt) * 0.02
-    t0 = time.perf_counter()
-    R.layer_subset(m, 1, hs, S, Kt, Vt, inplace=True, ctx=R.subset_ctx(m, S, T, dt))
-    parts["recompute"] = (time.perf_counter() - t0) * (nS / ns) * (L - 1)
-    # query sample: one layer for the query rows over the full cache
+    dev = R.deviation_score(k1, v1, K1[:, :, all_c], V1[:, :, all_c])[0]
+    top = dev.topk(budget).indices
+    S, order = all_c[top].sort()
+    hS = h[:, top][:, order]
+    parts["deviation"] = time.perf_counter() - t0
+    del h0, ctx, k1, v1
+    # one recompute layer over all selected rows against the full cache (timed on its second run)
+    for _ in range(2):
+        t0 = time.perf_counter()
+        R.layer_subset_rows(m, 1, hS, S, K1, V1, R.subset_ctx(m, S, T, dt))
+        t_layer = time.perf_counter() - t0
+    parts["recompute"] = t_layer * (L - 1)
+    # one layer of the query forward over the blended cache (T + n_query keys)
+    Kq, Vq = torch.cat([K1, mk(n_query)], dim=2), torch.cat([V1, mk(n_query)], dim=2)
     Sq = torch.arange(T, T + n_query)
-    hq = torch.randn(1, n_query, H, generator=g).to(dt) * 0.02
-    t0 = time.perf_counter()
-    R.layer_subset(m, 1, hq, Sq, Kc, Vc, inplace=True, ctx=R.subset_ctx(m, Sq, T + n_query, dt))
-    parts["query"] = (time.perf_counter() - t0) * L
+    hq = (torch.randn(1, n_query, H, generator=g) * 0.02).to(dt)
+    for _ in range(2):
+        t0 = time.perf_counter()
+        R.layer_subset(m, 1, hq, Sq, Kq, Vq, inplace=True, ctx=R.subset_ctx(m, Sq, T + n_query, dt))
+        parts["query"] = (time.perf_counter() - t0) * L
     total = sum(parts.values())
-    return {"value": round(total * 1e3, 1), "unit": "ms", "cores": threads, "kind": "port",
-            "sample": ("oracle (reference torch path restated, bf16) on host cores: assemble of 4/%d doc blocks "
-                       "x%d; deviation pass on 1%% of candidates x100; one recompute layer on 10%% of the %d "
-                       "selected rows x10 x%d layers; one query layer x%d; extrapolated"
-                       % (n_docs, n_docs // 4, nS, L - 1, L)),
-            "stages_ms": {k: round(v * 1e3, 1) for k, v in parts.items()}}
+    return {"value": round(total * 1e3, 1), "unit": "ms", "cores": threads, "kind": "port", "cpu": cpu_model(),
+            "sample": ("oracle (reference torch path restated, bf16) on %d host threads: assemble of all %d doc "
+                       "blocks and the deviation pass + top-k over all %d candidates in full; one recompute "
+                       "layer over all %d selected rows x%d layers and one query layer x%d extrapolated"
+                       % (threads, n_docs, n, budget, L - 1, L)),
+            "stages_ms": {k: round(v * 1e3, 1) for k, v in parts.items()},
+            "extrapolated_ms": round((parts["recompute"] + parts["query"]) * 1e3, 1),
+            "recompute_layer_ms": round(t_layer * 1e3, 1)}
 
 
 def main():
@@ -261,7 +323,11 @@ def main():
     ap.add_argument("--no-fold", action="store_true",
                     help="run the query forward after the recompute instead of inside it")
     ap.add_argument("--full-reps", type=int, default=3, help="full-prefill reps for the TTFT denominator (0: skip)")
-    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--cpu-threads", type=int, default=os.cpu_count() or 1)
+    ap.add_argument("--sweep", type=lambda v: [float(x) for x in v.split(",")] if v else [], default="0,0.2,0.5",
+                    help="recompute ratios timed after the headline (comma list; empty: skip), each with the "
+                         "first-token KL and top-1 against full prefill (bench/bench_scaling.py:68-72,88-91)")
+    ap.add_argument("--sweep-steps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode", type=int, default=32,
                     help="greedy decode steps timed after the TTFT loop on the last request's cache (0: skip)")
@@ -284,9 +350,14 @@ def main():
     from tread_amd import BlockStore, Engine, prefill_full
     from tread_amd.model import preset, synthetic_model
 
+    gemm_tables = None
     if not args.no_tune:
         from tread_amd.tuning import TABLE_7B, use_tuned_gemms
-        use_tuned_gemms(tables=() if args.retune else (TABLE_7B,), tune=bool(args.retune), out_file=args.retune)
+        gemm_tables = use_tuned_gemms(tables=() if args.retune else (TABLE_7B,), tune=bool(args.retune),
+                                      out_file=args.retune)
+        for t in gemm_tables:
+            log(f"[bench] GEMM solution table {t['table']}: {'in effect' if t['loaded'] else 'NOT in effect'}, "
+                f"{t['solutions']} solutions{'; stamps differ: ' + ', '.join(t['mismatched']) if t['mismatched'] else ''}")
     preset_name, n_docs, doc_len, n_sys, n_query = WORKLOADS[args.workload]
     cfg = preset(preset_name)
     dev = "cuda:0"
@@ -360,12 +431,19 @@ def main():
                     "frac": round(a_tf / BF16_MFMA_PEAK_TFLOPS, 4),
                     "traffic": MEASURED_ATTENTION_TRAFFIC.get(args.workload),
                     "avg_us": round(a_sec * 1e6, 2), "algorithmic_flop": a_flop}
-        full_ms = None
+        full_ms = full_logits = None
         if args.full_reps > 0:
             prefill_full(model, system, order, query)
-            fr = [prefill_full(model, system, order, query)[2].t["ttft"] for _ in range(args.full_reps)]
+            fr = []
+            for _ in range(args.full_reps):
+                full_logits, _, fst = prefill_full(model, system, order, query)
+                fr.append(fst.t["ttft"])
             full_ms = statistics.median(fr) * 1e3
             log(f"[bench] full prefill: {full_ms:.1f} ms")
+        sweep = None
+        if args.sweep and n_cold == 0:
+            sweep = ratio_sweep(eng, system, order, query, args.sweep, args.sweep_steps, full_ms, full_logits,
+                                headline=(args.ratio, ttfts))
         sec, nbytes = time_assemble(eng, system, docs, perm, n_query)
         gbs = nbytes / sec / 1e9
         log(f"[bench] assemble: {sec * 1e6:.1f} us, {gbs:.0f} GB/s")
@@ -394,12 +472,15 @@ def main():
                    "doc_len": doc_len, "system": n_sys, "query": n_query, "recompute_ratio": args.ratio,
                    "policy": "deviation", "hipgraph": not args.eager, "query_folded": not args.no_fold,
                    "gemm_tuning": not args.no_tune,
+                   "gemm_table_in_effect": None if gemm_tables is None else all(t["loaded"] for t in gemm_tables),
                    "gpu_tier_docs": n_docs if tier_docs is None else tier_docs, "cold_docs": n_cold,
                    "host_tier_hits_per_request": host_hits, "disk_tier": bool(args.disk_tier),
                    "parallelism": "single GPU"},
         "stages_ms": med,
         "ttft_full_prefill_ms": None if full_ms is None else round(full_ms, 2),
         "speedup_vs_full_prefill": None if full_ms is None else round(full_ms / ttft_ms, 2),
+        "sweep": sweep,
+        "gemm_tables": gemm_tables,
         "roofline": {"bound": "hbm", "kernel": "tread::rope_assemble_kernel", "achieved": round(gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": MEASURED_ASSEMBLE_TRAFFIC.get(args.workload), "avg_us": round(sec * 1e6, 2),

@@ -206,6 +206,24 @@ def layer_subset(m, l, h, S, K, V, inplace=False, ctx=None):
     return h, K, V
 
 
+def layer_subset_rows(m, l, h, S, K, V, ctx, chunk=4096):
+    """layer_subset with the attention and the MLP evaluated over chunks of `chunk` rows, so a
+    32 000-row deviation pass over a 32k cache stays within host memory; every fresh k/v is spliced
+    before any row attends, as in layer_subset (inplace). Row i's result depends on row i only
+    once the cache is spliced, so the chunking changes nothing (pinned against layer_subset)."""
+    (cos, sin), mask = ctx
+    x = M.norm(m, f"model.layers.{l}.input_layernorm", h)
+    q, k, v = M.qkv(m, l, x, cos, sin)
+    K[:, :, S], V[:, :, S] = k, v
+    out = torch.empty_like(h)
+    for a in range(0, h.shape[1], chunk):
+        b = min(a + chunk, h.shape[1])
+        o = M.o_proj(m, l, M.attend(m, q[:, :, a:b], K, V, mask[:, :, a:b]))
+        hc = h[:, a:b] + o
+        out[:, a:b] = hc + M.mlp(m, l, M.norm(m, f"model.layers.{l}.post_attention_layernorm", hc))
+    return out, K, V
+
+
 def deviation_score(k1, v1, K1c, V1c):
     """The score expression of tread/blend.py:129 on gathered cache rows: per-head L2 norm of the
     k and v differences, summed over heads, k part + v part (each op in the input dtype)."""

@@ -452,3 +452,20 @@ def test_small_model_cpu_fp32_reversed_reuse_of_4_docs():
     # of the reversed request at every doc position
     Kf, _ = R.prefill_kv(ref, torch.cat([system] + rev))
     assert torch.allclose(K[0][:, :, :64 + 1024], Kf[0], atol=1e-3)
+
+
+def test_row_chunked_layer_equals_layer_subset():
+    """The row-chunked recompute layer the CPU baseline times gives layer_subset's bits."""
+    from tread_amd.model import ModelConfig, synthetic_model
+    cfg = ModelConfig(512, 256, 2, 8, 2, 64, 384)
+    m = M.load(cfg, synthetic_model(cfg, "cpu", torch.bfloat16, seed=3).state_dict(), torch.bfloat16)
+    g = torch.Generator().manual_seed(5)
+    T = 700
+    S = torch.sort(torch.randperm(T, generator=g)[:300]).values
+    h = (torch.randn(1, 300, 256, generator=g) * 0.3).to(torch.bfloat16)
+    K = torch.randn(1, 2, T, 64, generator=g).to(torch.bfloat16)
+    V = torch.randn_like(K)
+    ctx = R.subset_ctx(m, S, T, torch.bfloat16)
+    want, Kw, Vw = R.layer_subset(m, 1, h, S, K.clone(), V.clone(), inplace=True, ctx=ctx)
+    got, Kg, Vg = R.layer_subset_rows(m, 1, h, S, K.clone(), V.clone(), ctx, chunk=64)
+    assert torch.equal(got, want) and torch.equal(Kg, Kw) and torch.equal(Vg, Vw)

@@ -16,10 +16,24 @@ import torch
 TABLE_7B = Path(__file__).resolve().with_name("gemm_gfx950_qwen2.5-7b.csv")
 
 
+def table_validators(path):
+    """The Validator lines (name -> value) a TunableOp table was stamped with."""
+    out = {}
+    for line in Path(path).read_text().splitlines():
+        parts = line.split(",", 2)
+        if len(parts) == 3 and parts[0] == "Validator":
+            out[parts[1]] = parts[2]
+    return out
+
+
 def use_tuned_gemms(tables=(TABLE_7B,), tune=False, out_file=None, max_tuning_ms=15, max_iterations=20):
     """Route torch GEMMs through TunableOp with the given solution tables. With tune=True, shapes
     not in the tables are benchmarked on first use (a one-off cost per shape) and written to
-    out_file; otherwise unknown shapes use the library default and nothing is written."""
+    out_file; otherwise unknown shapes use the library default and nothing is written.
+
+    Returns the status of each table: whether TunableOp accepted it (its torch / HIP / hipBLASLt /
+    rocBLAS / arch stamps match this process; otherwise every GEMM silently runs the library
+    default), how many solutions are in effect, and which stamps differ."""
     tun = torch.cuda.tunable
     tun.enable(True)
     tun.tuning_enable(bool(tune))
@@ -29,6 +43,16 @@ def use_tuned_gemms(tables=(TABLE_7B,), tune=False, out_file=None, max_tuning_ms
     # TunableOp may write its results at exit: keep that out of the working directory
     tun.set_filename(str(out_file) if (tune and out_file) else
                      str(Path(tempfile.gettempdir()) / f"tread_tunableop_{os.getpid()}.csv"))
+    status = []
     for t in tables:
-        if t and Path(t).exists():
-            tun.read_file(str(t))
+        if not t or not Path(t).exists():
+            status.append({"table": str(t), "loaded": False, "solutions": 0, "mismatched": ["missing file"]})
+            continue
+        ok = bool(tun.read_file(str(t)))
+        have = dict(tun.get_validators())
+        want = table_validators(t)
+        mismatched = sorted(k for k, v in want.items() if k in have and have[k] != v)
+        n = len(tun.get_results())
+        status.append({"table": Path(t).name, "loaded": ok and not mismatched and n > 0, "solutions": n,
+                       "mismatched": mismatched})
+    return status
