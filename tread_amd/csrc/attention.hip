@@ -591,11 +591,15 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
         settle(j, sc);
         to_p(sc, pb);
       }
-      // the scores of tile j are in pb now, so sc takes tile j + 1's
+      // the scores of tile j are in pb now, so sc takes tile j + 1's. The MFMA phase runs at raised
+      // wave priority, so its MFMAs and fragment reads issue ahead of the partner wave's softmax
+      // VALU work on the same SIMD (measured 0.7-1 % faster on the recompute and causal shapes).
+      __builtin_amdgcn_s_setprio(1);
       qk(bn, sc);
       s16x4_t v0[NV];
       v_read(std::integral_constant<int, 0>{}, (uint32_t)(bj * SM::BUF * 2), v0);
       pv(bj, pb, v0);
+      __builtin_amdgcn_s_setprio(0);
       ++j;
       bj = bn;
       if (!late) {
