@@ -40,9 +40,18 @@ GPU_TIER_DOCS = {"qwen2.5-1.5b-16k": 8}
 # docs per request that are not cached (fresh token ids every request): they go through the packed
 # block-diagonal prefill inside the timed request
 COLD_DOCS = {"llama3-70b-32k": 8}
+# the request's doc order: a seeded permutation unless named here
+ORDER = {"qwen2.5-0.5b-1k": "reversed"}
+# recompute ratio when --ratio is not given (0.2 otherwise)
+DEFAULT_RATIO = {"qwen2.5-0.5b-1k": 0.0}
+# workloads whose CPU baseline runs the oracle's whole request end to end (the dtype it runs in);
+# the others time its stages on the request's sizes
+E2E_CPU = {"qwen2.5-0.5b-1k": torch.float32, "qwen2.5-0.5b-8k": torch.bfloat16,
+           "qwen2.5-1.5b-16k": torch.bfloat16}
 WORKLOADS = {
     # name: (preset, n_docs, doc_len, n_system, n_query)
     "qwen2.5-7b-32k": ("qwen2.5-7b", 32, 1000, 64, 32),
+    "qwen2.5-0.5b-1k": ("qwen2.5-0.5b", 4, 256, 64, 32),
     "qwen2.5-1.5b-16k": ("qwen2.5-1.5b", 16, 1000, 64, 32),
     "qwen2.5-0.5b-8k": ("qwen2.5-0.5b", 8, 1000, 64, 32),
     "llama3-70b-32k": ("llama3-70b", 32, 1000, 64, 32),
@@ -53,13 +62,16 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def make_inputs(cfg, n_docs, doc_len, n_sys, n_query, device):
+def make_inputs(cfg, n_docs, doc_len, n_sys, n_query, device, order=None):
     g = torch.Generator().manual_seed(1)
     V = cfg.vocab_size
     system = torch.randint(0, V, (n_sys,), generator=g)
     docs = [torch.randint(0, V, (doc_len,), generator=g) for _ in range(n_docs)]
     query = torch.randint(0, V, (n_query,), generator=g)
-    perm = torch.randperm(n_docs, generator=torch.Generator().manual_seed(2)).tolist()
+    if order == "reversed":
+        perm = list(range(n_docs))[::-1]
+    else:
+        perm = torch.randperm(n_docs, generator=torch.Generator().manual_seed(2)).tolist()
     to = lambda t: t.to(device)
     return to(system), [to(d) for d in docs], to(query), perm
 
@@ -200,6 +212,39 @@ def ratio_sweep(eng, system, order, query, ratios, steps, full_ms, full_logits, 
     return out
 
 
+def cpu_baseline_e2e(model, cfg, system, docs, query, perm, ratio, dtype, threads, budget, cpu_budget):
+    """The oracle's whole request (the reference's torch path restated, tread/engine.py:98-136) on
+    this machine's host cores, on the same weights (copied from the GPU model, in `dtype`) and the
+    same ids: a cold pass over the docs in order fills its store (untimed), then warm requests in
+    the benchmark's doc order; TTFT = median of the timed ones (5 after 2 warm-ups; 3 after 1 when
+    a request takes over 10 s)."""
+    from oracle import tread_ref as R
+    torch.set_num_threads(threads)
+    ref = R.M.load(cfg, {k: v.detach().to("cpu") for k, v in model.state_dict().items()}, dtype)
+    eng = R.Engine(ref, R.BlockStore(budget, cpu_budget))
+    cpu = lambda t: t.to("cpu")
+    sysc, docc, qc = cpu(system), [cpu(d) for d in docs], cpu(query)
+    order = [docc[i] for i in perm]
+    eng.prefill(sysc, docc, qc)
+    t0 = time.perf_counter()
+    _, _, st = eng.prefill(sysc, order, qc, ratio=ratio)
+    first = time.perf_counter() - t0
+    warm, reps = (1, 3) if first > 10 else (2, 5)
+    for _ in range(warm - 1):
+        eng.prefill(sysc, order, qc, ratio=ratio)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        _, _, st = eng.prefill(sysc, order, qc, ratio=ratio)
+        times.append(time.perf_counter() - t0)
+    ms = statistics.median(times) * 1e3
+    return {"value": round(ms, 1), "unit": "ms", "cores": threads, "kind": "port", "cpu": cpu_model(),
+            "sample": (f"oracle (reference torch path restated, {str(dtype).split('.')[-1]}) end to end on {threads} "
+                       f"host threads: the whole warm request (hits {st.hits}, misses {st.misses}), median of {reps} "
+                       f"after {warm} warm-up(s); same weights and ids as the GPU run"),
+            "reps_ms": [round(t * 1e3, 1) for t in times]}
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -318,7 +363,8 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="qwen2.5-7b-32k", choices=list(WORKLOADS))
-    ap.add_argument("--ratio", type=float, default=0.2)
+    ap.add_argument("--ratio", type=float, default=None,
+                    help="recompute ratio (default: the workload's, 0.2 unless named in DEFAULT_RATIO)")
     ap.add_argument("--eager", action="store_true", help="recompute loop without the hipGraph")
     ap.add_argument("--no-fold", action="store_true",
                     help="run the query forward after the recompute instead of inside it")
@@ -359,12 +405,14 @@ def main():
             log(f"[bench] GEMM solution table {t['table']}: {'in effect' if t['loaded'] else 'NOT in effect'}, "
                 f"{t['solutions']} solutions{'; stamps differ: ' + ', '.join(t['mismatched']) if t['mismatched'] else ''}")
     preset_name, n_docs, doc_len, n_sys, n_query = WORKLOADS[args.workload]
+    if args.ratio is None:
+        args.ratio = DEFAULT_RATIO.get(args.workload, 0.2)
     cfg = preset(preset_name)
     dev = "cuda:0"
     torch.cuda.set_device(0)
     log(f"[bench] building {preset_name} (random init on the GPU)")
     model = synthetic_model(cfg, dev, torch.bfloat16, seed=0)
-    system, docs, query, perm = make_inputs(cfg, n_docs, doc_len, n_sys, n_query, dev)
+    system, docs, query, perm = make_inputs(cfg, n_docs, doc_len, n_sys, n_query, dev, ORDER.get(args.workload))
     T = n_sys + n_docs * doc_len
     tier_docs = GPU_TIER_DOCS.get(args.workload) if args.gpu_tier_docs is None else args.gpu_tier_docs
     if tier_docs is not None and tier_docs < 0:
@@ -451,10 +499,15 @@ def main():
     ttft_ms = statistics.median(ttfts) * 1e3
     med = {k: round(statistics.median(s[k] for s in stages) * 1e3, 2) for k in stages[0]}
     cpu = None
-    if not args.no_cpu:
-        log("[bench] cpu baseline (oracle, bounded sample)")
+    if not args.no_cpu and args.workload in E2E_CPU and n_cold == 0:
+        log("[bench] cpu baseline (oracle, the whole request)")
+        cpu = cpu_baseline_e2e(model, cfg, system, docs, query, perm, args.ratio, E2E_CPU[args.workload],
+                               args.cpu_threads, budget, 1 << 40)
+        log(f"[bench] cpu baseline: {cpu['value']} ms")
+    elif not args.no_cpu:
+        log("[bench] cpu baseline (oracle, stage by stage)")
         cpu = cpu_baseline(preset_name, n_docs, doc_len, n_sys, n_query, args.ratio, args.cpu_threads)
-        log(f"[bench] cpu baseline: {cpu['value']} ms extrapolated")
+        log(f"[bench] cpu baseline: {cpu['value']} ms (partly extrapolated)")
     out = {
         "metric": METRIC,
         "value": round(ttft_ms, 2),

@@ -203,3 +203,31 @@ def test_promoted_blocks_stop_pending_and_take_the_fused_launch(models):
     finally:
         _hip.rope_assemble = orig
     assert calls == [0] and torch.equal(got2, want)  # one fused launch, no per-layer assembly
+
+
+def test_plain_reuse_replays_the_query_forward_from_a_graph(models):
+    """A request that recomputes nothing (ratio 0) replays its query forward from a graph captured
+    over a query-only cache bucket: logits bit-identical to the eager forward, the cache decodes,
+    and SubsetRunner.captures still counts only recompute-loop graphs (tests/test_engine.py:109
+    expects 1 after a ratio-0 pass and two graphed requests)."""
+    gpu, _ = models
+    prefix, docs, query = _request(7)
+    on = lambda x: [t.to(DEV) for t in x] if isinstance(x, list) else x.to(DEV)
+    eager = Engine(gpu, BlockStore(1 << 30))
+    graphed = Engine(gpu, BlockStore(1 << 30), graphs=True)
+    for e in (eager, graphed):
+        e.prefill(on(prefix), on(docs), on(query))
+    a, ca, _ = eager.prefill(on(prefix), on(docs[::-1]), on(query), reserve=3)
+    for _ in range(2):
+        b, cb, _ = graphed.prefill(on(prefix), on(docs[::-1]), on(query), reserve=3)
+    assert cb.graph is not None and graphed.runner.query_captures == 1 and graphed.runner.captures == 0
+    assert torch.equal(a, b)
+    n = ca.length
+    assert torch.equal(ca.K[..., :n, :], cb.K[..., :n, :]) and torch.equal(ca.V[..., :n, :], cb.V[..., :n, :])
+    nxt = torch.tensor([int(a.argmax())], device=DEV)
+    assert torch.equal(eager.decode(ca, nxt), graphed.decode(cb, nxt))
+    fresh = Engine(gpu, graphed.store, graphs=True)  # the reference test's sequence on a new runner
+    fresh.prefill(on(prefix), on(docs), on(query))
+    for _ in range(2):
+        fresh.prefill(on(prefix), on(docs[::-1]), on(query), ratio=0.2)
+    assert fresh.runner.captures == 1 and fresh.runner.query_captures == 1  # the reference's count

@@ -197,12 +197,14 @@ class Engine:
         Nq = len(query_ids)
         dev = prefix_ids.device
         graph = None
-        if ratio > 0 and self.runner is not None and docs and self.runner.worth_it(T):
-            n, budget = select(ratio, docs)
+        if self.runner is not None and self.runner.worth_it(T):
+            budget = select(ratio, docs)[1] if (ratio > 0 and docs) else 0
             if budget > 0:
                 start = 1 if policy == "deviation" else 0
                 graph = self.runner.cache_for(start, budget, T, Nq, dev, room=Nq + reserve,
                                               fold=self.fold_query and Nq > 0)
+            elif Nq > 0:  # nothing to recompute: the query forward alone is replayed
+                graph = self.runner.query_cache_for(T, Nq, dev, room=Nq + reserve)
         if graph is not None:
             K, V = graph.K, graph.V
         else:

@@ -141,6 +141,20 @@ class _Graph:
         self.out = carry["out"][-1]
 
 
+class _QueryBucket:
+    """A cache bucket without a recompute loop: a request that recomputes nothing (ratio 0, or a
+    budget that rounds to 0) only replays the query forward captured over this bucket's cache."""
+
+    def __init__(self, P, Tb, t_cap, device):
+        self.t_cap, self.Tb, self.nb, self.nq = t_cap, Tb, 0, 0
+        self.generation = 0
+        self.queries = {}
+        self.K, self.V = alloc_cache(P, t_cap, device)
+        self.K.zero_()
+        self.V.zero_()
+        self.Kl, self.Vl = self.K.unbind(0), self.V.unbind(0)
+
+
 class SubsetRunner:
     """One captured graph per (start layer, rows bucket, cache bucket, query room); LRU of
     `max_graphs`. `max_ctx`: contexts above it run eagerly (None: always graph)."""
@@ -154,7 +168,8 @@ class SubsetRunner:
         self.trim_last = trim_last
         self.seg = seg
         self.graphs: "OrderedDict[tuple, _Graph]" = OrderedDict()
-        self.captures = 0
+        self.captures = 0  # graphs of the recompute loop (tread/graphs.py's count, tests/test_engine.py:109)
+        self.query_captures = 0  # query forwards captured for requests that recompute nothing
 
     def worth_it(self, T):
         return self.max_ctx is None or T <= self.max_ctx
@@ -188,6 +203,27 @@ class SubsetRunner:
             if nqb not in g.queries:
                 g.queries[nqb] = _QueryGraph(self.P, g, nqb, device)
                 self.captures += 1
+        return g
+
+    @torch.inference_mode()
+    def query_cache_for(self, T, n_query, device, room=None, t_step=1024):
+        """The bucket serving a request that recomputes nothing over a T-row context: its .K/.V
+        are the cache to assemble into, and the query forward for n_query rows is captured over it
+        (before anything is assembled); rows after the context: room >= n_query (for decoding)."""
+        Tb = -(-T // t_step) * t_step
+        key = ("query", Tb, _q_room(max(n_query, room or 0)))
+        g = self.graphs.get(key)
+        if g is None:
+            while len(self.graphs) >= self.max_graphs:
+                self.graphs.popitem(last=False)
+            g = _QueryBucket(self.P, Tb, Tb + key[2], device)
+            self.graphs[key] = g
+        self.graphs.move_to_end(key)
+        g.generation += 1  # a cache handed out for this bucket earlier is about to be overwritten
+        nqb = _q_bucket(n_query)
+        if nqb not in g.queries:
+            g.queries[nqb] = _QueryGraph(self.P, g, nqb, device)
+            self.query_captures += 1  # not in `captures`, which counts the recompute loop's graphs
         return g
 
     @torch.inference_mode()
