@@ -1,14 +1,19 @@
 // (a) Fused RoPE re-rotation + gather/append of cached KV blocks into the assembled cache.
 //
-// One streaming pass over HBM: every source row is read once and written once. A work unit is
-// (source, layer, kv head, 16 token rows for hd 128); within a unit the source rows and the
-// destination rows are each one contiguous span, so K and V move as 16-byte vectors with
-// non-temporal loads and stores. Units are small and many (~10^5 per request) and each thread
-// issues all of its loads before its first store, the shape that reaches the copy ceiling. A
-// rotated K row is processed as pairs of 16-byte vectors (j, j + hd/2), the two halves that
-// rotate_half mixes, one pair per thread. cos/sin come from a per-source fp32 table (the caller
-// builds it exactly as the reference's rotary embedding does; 512 B per source, cache resident).
-// The rotation keeps the reference's fp32 op order with no contraction,
+// One streaming pass over HBM: every source row is read once and written once. Within a work unit
+// (source, layer, kv head, a span of token rows) the source rows and the destination rows are each
+// one contiguous span, so K and V move as 16-byte vectors with non-temporal loads and stores.
+//  - head_dim 128 (`rope_assemble_kernel`): a unit is 16 token rows of ONE tensor, K or V, and
+//    thread t moves chunk t of that 4 KiB span: the one-chunk-per-thread, one-stream-per-group
+//    shape of the fastest plain copy on this part (the 7B request's bytes without rotation:
+//    6.1 TB/s, against 5.4-5.8 with K and V in one group). rotate_half's partner of K chunk j is
+//    chunk j ^ 8 of the same row, i.e. lane l ^ 8 within a 16-lane DPP row (row_ror:8). The
+//    source's cos/sin table (512 B) is staged in LDS once per group: read from the cache by every
+//    thread it would be 4x the unit's own bytes (measured 730 vs 627 us per request).
+//  - head_dim 64 (`rope_assemble_pairs_kernel`): a unit is 32 token rows of K and V; each thread
+//    moves one V chunk and, on half of the threads, one K pair (j, j + hd/2).
+// cos/sin come from a per-source fp32 table that the caller builds exactly as the reference's
+// rotary embedding does. The rotation keeps the reference's fp32 op order with no contraction,
 // fl(fl(x1*c) + fl(-x2*s)) and fl(fl(x2*c) + fl(x1*s)), then one RNE to bf16.
 #include "common.h"
 #include "../../include/tread_hip.h"
@@ -43,36 +48,111 @@ struct AsmArgs {
   int32_t pad;
 };
 
-// Rows per work unit: one 16-byte V chunk per thread; rotation pairs (8 + 8 K elements) on the
-// first half of the threads.
+// Rows per work unit: one 16-byte chunk per thread of one row span (hd 128: K or V; hd 64: the V
+// span, with the K pairs on the first half of the threads).
 template <int HD>
 constexpr int asm_rows() { return ASM_THREADS / (HD / 8); }
 
+// The unit's source (binary search over the sources' first units) and its row spans.
+struct AsmUnit {
+  int s;          // source index
+  int rows;       // valid rows of the unit
+  int64_t soff;   // element offset of the unit's first row in the source's K (and V)
+  int64_t doff;   // element offset of its first destination row in the cache
+};
 template <int HD>
-__global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArgs a) {
-  constexpr int HALF = HD / 2;
-  constexpr int PG = HALF / 8;               // pair groups per K row
-  constexpr int ROWS = asm_rows<HD>();       // 16 (hd 128) or 32 (hd 64)
-  constexpr int V_PER_T = ROWS * (HD / 8) / ASM_THREADS;  // 16-byte chunks per thread: 1
-
-  const int u = blockIdx.x;
-  if (u >= a.total_units) return;
+__device__ __forceinline__ AsmUnit asm_unit(const AsmArgs& a, int u) {
+  constexpr int ROWS = asm_rows<HD>();
   int lo = 0, hi = a.n_src - 1;  // last source whose first unit is <= u
   while (lo < hi) {
     int mid = (lo + hi + 1) >> 1;
     if (a.src[mid].unit_begin <= u) lo = mid; else hi = mid - 1;
   }
-  const int s = lo;
-  const AsmSrc& src = a.src[s];
+  const AsmSrc& src = a.src[lo];
   const int local = u - src.unit_begin;
   const int chunk = local % src.chunks;
   const int lh = local / src.chunks;
   const int head = lh % a.n_kv;
   const int layer = a.layer_lo + lh / a.n_kv;
   const int64_t row0 = (int64_t)chunk * ROWS;
-  const int rows = (int)min<int64_t>(ROWS, src.n - row0);
-  const int64_t soff = (((int64_t)layer * a.n_kv + head) * src.n + row0) * HD;
-  const int64_t doff = (((int64_t)layer * a.n_kv + head) * a.t_cap + src.dst_off + row0) * HD;
+  AsmUnit r;
+  r.s = lo;
+  r.rows = (int)min<int64_t>(ROWS, src.n - row0);
+  r.soff = (((int64_t)layer * a.n_kv + head) * src.n + row0) * HD;
+  r.doff = (((int64_t)layer * a.n_kv + head) * a.t_cap + src.dst_off + row0) * HD;
+  return r;
+}
+
+// lane l ^ 8 of the same 16-lane row (DPP row_ror:8)
+__device__ __forceinline__ uint32_t lane_xor8(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
+}
+
+// head_dim 128. Work group b is unit b / 2, its K span for even b and its V span for odd b (K
+// only, one group per unit, when the launch moves no V).
+__global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArgs a) {
+  constexpr int HD = 128, HALF = HD / 2, CH = HD / 8;  // 16 chunks per row, 16 rows per unit
+  const bool has_v = a.dv != nullptr;  // uniform: a K-only launch (rotate_keys) moves no V
+  const int b = blockIdx.x;
+  const int u = has_v ? b >> 1 : b;
+  if (u >= a.total_units) return;
+  const bool is_v = has_v && (b & 1);
+  const AsmUnit w = asm_unit<HD>(a, u);
+  const AsmSrc& src = a.src[w.s];
+  const int c = threadIdx.x, r = c / CH;
+  const bool ok = r < w.rows;
+  if (is_v) {
+    if (ok) stg_nt(reinterpret_cast<u32x4_t*>(a.dv + w.doff) + c, ldg_nt(reinterpret_cast<const u32x4_t*>(src.v + w.soff) + c));
+    return;
+  }
+  u32x4_t x = {0, 0, 0, 0};
+  if (ok) x = ldg_nt(reinterpret_cast<const u32x4_t*>(src.k + w.soff) + c);
+  if (src.delta == 0) {  // a bit copy
+    if (ok) stg_nt(reinterpret_cast<u32x4_t*>(a.dk + w.doff) + c, x);
+    return;
+  }
+  __shared__ f32x4_t tab_s[HALF * 2 / 4];  // (cos, sin) of the source's 64 columns
+  if (c < HALF * 2 / 4) tab_s[c] = reinterpret_cast<const f32x4_t*>(a.cos_sin + (int64_t)w.s * HALF * 2)[c];
+  __syncthreads();
+  const int j = c % CH;
+  const int g = (j & 7) * 4;  // columns (j & 7) * 8 .. + 7
+  const f32x4_t t0 = tab_s[g], t1 = tab_s[g + 1], t2 = tab_s[g + 2], t3 = tab_s[g + 3];
+  u32x4_t p;  // partner chunk j ^ 8 (every lane of the row takes part, valid or not)
+#pragma unroll
+  for (int q = 0; q < 4; ++q) p[q] = lane_xor8(x[q]);
+  if (!ok) return;
+  const float cv[8] = {t0[0], t0[2], t1[0], t1[2], t2[0], t2[2], t3[0], t3[2]};
+  const float sv[8] = {t0[1], t0[3], t1[1], t1[3], t2[1], t2[3], t3[1], t3[3]};
+  // own chunk y, partner q: first half (j < 8) y c + (-q) s, second half y c + q s
+  const float sg = j < 8 ? -1.f : 1.f;
+  u32x4_t o;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float cl = cv[2 * q], ch = cv[2 * q + 1], sl = sv[2 * q], sh = sv[2 * q + 1];
+    const float yl = lo_bf(x[q]), yh = hi_bf(x[q]);
+    const float pl = sg * lo_bf(p[q]), ph = sg * hi_bf(p[q]);
+    {
+#pragma clang fp contract(off)
+      o[q] = pack_bf(yl * cl + pl * sl, yh * ch + ph * sh);
+    }
+  }
+  stg_nt(reinterpret_cast<u32x4_t*>(a.dk + w.doff) + c, o);
+}
+
+// head_dim 64
+template <int HD>
+__global__ __launch_bounds__(ASM_THREADS) void rope_assemble_pairs_kernel(const AsmArgs a) {
+  constexpr int HALF = HD / 2;
+  constexpr int PG = HALF / 8;               // pair groups per K row
+  constexpr int ROWS = asm_rows<HD>();       // 32 (hd 64)
+  constexpr int V_PER_T = ROWS * (HD / 8) / ASM_THREADS;  // 16-byte chunks per thread: 1
+
+  const int u = blockIdx.x;
+  if (u >= a.total_units) return;
+  const AsmUnit w = asm_unit<HD>(a, u);
+  const int s = w.s, rows = w.rows;
+  const int64_t soff = w.soff, doff = w.doff;
+  const AsmSrc& src = a.src[s];
   const int tid = threadIdx.x;
   const int nvec = rows * HD / 8;  // valid 16-byte chunks of this unit's K or V span
   const bool has_v = a.dv != nullptr;  // uniform: a K-only launch (rotate_keys) moves no V
@@ -200,11 +280,14 @@ extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void
     a.layer_lo = layer_lo;
     a.n_lr = n_lr;
     a.total_units = (int32_t)units;
-    dim3 grid((unsigned)units), block(ASM_THREADS);
+    // hd 128: one work group per unit and tensor (K, V)
+    const int64_t groups = head_dim == 128 && dst_v ? 2 * units : units;
+    if (groups > 0x7fffffffLL) return fail(TREAD_ERANGE, "rope_assemble: too many work units");
+    dim3 grid((unsigned)groups), block(ASM_THREADS);
     if (head_dim == 128)
-      hipLaunchKernelGGL(rope_assemble_kernel<128>, grid, block, 0, (hipStream_t)stream, a);
+      hipLaunchKernelGGL(rope_assemble_kernel, grid, block, 0, (hipStream_t)stream, a);
     else
-      hipLaunchKernelGGL(rope_assemble_kernel<64>, grid, block, 0, (hipStream_t)stream, a);
+      hipLaunchKernelGGL(rope_assemble_pairs_kernel<64>, grid, block, 0, (hipStream_t)stream, a);
     int rc = check_launch("rope_assemble");
     if (rc) return rc;
   }
