@@ -697,12 +697,21 @@ __global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(const AttnArg
   for (int q = 0; q < CMB_THREADS / 64; ++q) L += red[q];
   // this thread's 4 elements over its split group
   const int dq = t % DQ, sg = t / DQ;
+  // the group's slices four at a time: their loads go out together, the sum keeps slice order
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s = sg; s < a.nsplit; s += SG) {
-    const float wgt = sm_w[s];
-    if (wgt == 0.f) continue;
-    const f32x4_t o = *reinterpret_cast<const f32x4_t*>(a.ws_o + (p0 + s * stride) * HD + dq * 4);
-    acc += wgt * o;
+  constexpr int UNR = 4;
+  for (int s0 = sg; s0 < a.nsplit; s0 += UNR * SG) {
+    f32x4_t o[UNR];
+    float wg[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int s = s0 + u * SG;
+      wg[u] = s < a.nsplit ? sm_w[s] : 0.f;
+      if (wg[u] != 0.f) o[u] = *reinterpret_cast<const f32x4_t*>(a.ws_o + (p0 + s * stride) * HD + dq * 4);
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+      if (wg[u] != 0.f) acc += wg[u] * o[u];
   }
   part[sg][dq] = acc;
   __syncthreads();
@@ -772,23 +781,36 @@ __global__ __launch_bounds__(HALF_ROWS * 64) void attn_combine_few_kernel(const 
   const int tile = (int)(r / ATT_BM), in_tile = (int)(r % ATT_BM);
   const int64_t stride = (int64_t)a.hkv * a.tiles * ATT_BM;
   const int64_t p0 = ((int64_t)head * a.tiles + tile) * ATT_BM + in_tile;
-  float M = -INFINITY;
-  for (int sp = 0; sp < a.nsplit; ++sp) {
-    const int64_t p = p0 + sp * stride;
-    if (a.ws_ml[p * 2 + 1] > 0.f) M = fmaxf(M, a.ws_ml[p * 2]);
+  // every slice's (max, sum) and partial O are loaded up front (one round of memory latency, not
+  // one per slice); the merge then walks the slices in order
+  float mv[CMB_FEW_SPLITS], lv[CMB_FEW_SPLITS], ov[CMB_FEW_SPLITS][EPL];
+#pragma unroll
+  for (int sp = 0; sp < CMB_FEW_SPLITS; ++sp) {
+    if (sp < a.nsplit) {
+      const int64_t p = p0 + sp * stride;
+      const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + p * 2);
+      mv[sp] = ml.x;
+      lv[sp] = ml.y;
+      const float* o = a.ws_o + p * HD + lane * EPL;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) ov[sp][e] = o[e];
+    }
   }
+  float M = -INFINITY;
+#pragma unroll
+  for (int sp = 0; sp < CMB_FEW_SPLITS; ++sp)
+    if (sp < a.nsplit && lv[sp] > 0.f) M = fmaxf(M, mv[sp]);
   float L = 0.f, acc[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  for (int sp = 0; sp < a.nsplit; ++sp) {
-    const int64_t p = p0 + sp * stride;
-    const float l = a.ws_ml[p * 2 + 1];
-    if (!(l > 0.f)) continue;
-    const float wgt = __builtin_amdgcn_exp2f(a.ws_ml[p * 2] - M);
-    L += wgt * l;
-    const float* o = a.ws_o + p * HD + lane * EPL;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] += wgt * o[e];
+  for (int sp = 0; sp < CMB_FEW_SPLITS; ++sp) {
+    if (sp < a.nsplit && lv[sp] > 0.f) {
+      const float wgt = __builtin_amdgcn_exp2f(mv[sp] - M);
+      L += wgt * lv[sp];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] += wgt * ov[sp][e];
+    }
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   const int64_t qi = r / a.G;
