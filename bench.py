@@ -387,6 +387,8 @@ def main():
                          "tread_amd/tuning, applied through PyTorch TunableOp)")
     ap.add_argument("--retune", default=None, metavar="OUT_CSV",
                     help="benchmark GEMM solutions for every shape met (warm-up absorbs it) and write them here")
+    ap.add_argument("--gemm-table", default=None, metavar="CSV",
+                    help="GEMM solution table to apply instead of tread_amd/tuning's 7B table")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU: there is no multi-GPU path (asked for {args.gpus}); "
@@ -399,7 +401,8 @@ def main():
     gemm_tables = None
     if not args.no_tune:
         from tread_amd.tuning import TABLE_7B, use_tuned_gemms
-        gemm_tables = use_tuned_gemms(tables=() if args.retune else (TABLE_7B,), tune=bool(args.retune),
+        table = args.gemm_table or TABLE_7B
+        gemm_tables = use_tuned_gemms(tables=() if args.retune else (table,), tune=bool(args.retune),
                                       out_file=args.retune)
         for t in gemm_tables:
             log(f"[bench] GEMM solution table {t['table']}: {'in effect' if t['loaded'] else 'NOT in effect'}, "
