@@ -82,6 +82,33 @@ def test_rope_assemble_matches_fp32_rotation_and_cat_layout(hd, kv, L):
     assert ours.float().mean().item() < theirs.float().mean().item()
 
 
+@pytest.mark.parametrize("hd", [128, 64])
+def test_rope_assemble_more_sources_than_one_launch_holds(hd):
+    """More sources than one launch carries (48): the library splits the list into launches, each
+    with its own slice of the cos/sin table; every source lands rotated, in cat order."""
+    g = torch.Generator().manual_seed(12)
+    m = _ref_model(hd)
+    L, kv, n_src = 2, 2, 61
+    lens = [1 + (7 * i) % 40 for i in range(n_src)]
+    t_cap = sum(lens) + 16
+    srcs, exp_K, exp_V, off = [], [], [], 0
+    for i, n in enumerate(lens):
+        K = (2 * torch.randn(L, 1, kv, n, hd, generator=g)).to(torch.bfloat16)
+        V = torch.randn(L, 1, kv, n, hd, generator=g).to(torch.bfloat16)
+        delta = off - 3 * i  # a different shift per source
+        srcs.append((K, V, off, delta))
+        exp_K.append(R.rotate_keys_fp32(m, K, delta))
+        exp_V.append(V)
+        off += n
+    dK = torch.zeros(L, 1, kv, t_cap, hd, dtype=torch.bfloat16, device=DEV)
+    dV = torch.zeros_like(dK)
+    _hip.rope_assemble([(K.to(DEV), V.to(DEV), o, d) for K, V, o, d in srcs], dK, dV, m.inv_freq)
+    torch.cuda.synchronize()
+    assert torch.equal(dV[..., :off, :].cpu(), torch.cat(exp_V, dim=-2))
+    u = bf16_ulps(dK[..., :off, :].cpu(), torch.cat(exp_K, dim=-2))
+    assert u.max().item() == 0, (u.max(), (u > 0).sum())
+
+
 def _rotate_fp64(m, K, delta):
     n = K.shape[-2]
     freqs = (m.inv_freq[:, None].float() @ torch.full((1, n), float(delta))).transpose(0, 1).double()
