@@ -216,6 +216,7 @@ class Engine:
             offset += len(d)
         cands = list(torch.arange(Pn, T, device=dev).split([len(d) for d in docs])) if docs else []
         asm = _Assembly(self.P, K, V, sources)
+        hook = asm.ensure if asm.pending else None  # None: nothing to wait for between layers
         Kl, Vl = K.unbind(0), V.unbind(0)
         self._sync()
         t1 = time.perf_counter()
@@ -227,21 +228,21 @@ class Engine:
             if self.fold_query and Nq > 0:  # the query rows ride in the recompute (blend_query)
                 self.last_selected, st.recompute_eff, logits = blend_query(
                     self.model, ctx, Kl, Vl, cands, ratio, policy, query_ids, T, gen=gen, runner=self.runner,
-                    graph=graph, hook=asm.ensure)
+                    graph=graph, hook=hook)
             else:
                 self.last_selected, st.recompute_eff = blend_cache(
                     self.model, ctx, Kl, Vl, cands, ratio, policy, gen=gen, runner=self.runner, graph=graph, T=T,
-                    hook=asm.ensure)
+                    hook=hook)
         self._sync()
         t2 = time.perf_counter()
 
         if logits is not None:
             logits = logits.clone()  # a graph's output is static
         elif graph is not None and Nq > 0:
-            logits = self.runner.query(graph, query_ids, T, hook=asm.ensure).clone()  # the graph's output is static
+            logits = self.runner.query(graph, query_ids, T, hook=hook).clone()  # the graph's output is static
         else:
             R = make_rows(self.P, torch.arange(T, T + Nq, device=dev))
-            h, d = run_layers(self.P, embed(self.P, query_ids), None, R, Kl, Vl, range(self.P.L), hook=asm.ensure)
+            h, d = run_layers(self.P, embed(self.P, query_ids), None, R, Kl, Vl, range(self.P.L), hook=hook)
             logits = final_logits(self.P, h, d)
         self._sync()
         t3 = time.perf_counter()
