@@ -123,7 +123,7 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArg
   if (!ok) return;
   const float cv[8] = {t0[0], t0[2], t1[0], t1[2], t2[0], t2[2], t3[0], t3[2]};
   const float sv[8] = {t0[1], t0[3], t1[1], t1[3], t2[1], t2[3], t3[1], t3[3]};
-  // own chunk y, partner q: first half (j < 8) y c + (-q) s, second half y c + q s
+  // own chunk y, partner chunk p: first half (j < 8) y c + (-p) s, second half y c + p s
   const float sg = j < 8 ? -1.f : 1.f;
   u32x4_t o;
 #pragma unroll
