@@ -23,7 +23,7 @@ typedef void* tread_event_t;  /* hipEvent_t */
 
 /* Thread-local text of the last error (empty string if none). */
 const char* tread_last_error(void);
-/* ABI version of this header (8); bumps on any signature change. */
+/* ABI version of this header (9); bumps on any signature change. */
 int tread_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------
@@ -162,6 +162,20 @@ int tread_skinny_linear_bf16(const void* x, int64_t ldx, const void* weight, con
 int tread_skinny_norm_linear_bf16(const void* h, const void* delta, const void* ln_weight, float eps, int64_t m,
                                   int64_t n, int64_t k, const void* weight, const void* bias, void* y, void* h_out,
                                   tread_stream_t stream);
+
+/* skinny_norm_linear of the q|k|v projection with tread_qkv_rope_splice_bf16 fused behind it:
+ * qkv = linear(RMSNorm(h + delta), wqkv, bqkv) for m <= 8 rows (wqkv: [(hq + 2 hkv) head_dim,
+ * hidden], bqkv may be NULL), then q and k rotated with cos / sin [m, head_dim / 2], q into q_out
+ * [m, hq, head_dim], k and v into row rows[i] of k_cache / v_cache [hkv, t_cap, head_dim] (rows
+ * outside [0, t_cap) splice nothing), h_out = h + delta (may be NULL). Bits equal to
+ * tread_skinny_norm_linear_bf16 followed by tread_qkv_rope_splice_bf16, in one launch. Replaces
+ * the input_layernorm + q/k/v projections + apply_rotary_pos_emb + cache update of a decoding step
+ * (transformers Qwen2Attention under tread/server.py:207).
+ */
+int tread_skinny_norm_qkv_rope_bf16(const void* h, const void* delta, const void* ln_weight, float eps, int64_t m,
+                                    int64_t hidden, const void* wqkv, const void* bqkv, int hq, int hkv, int head_dim,
+                                    const void* cos, const void* sin, const int64_t* rows, void* q_out, void* k_cache,
+                                    void* v_cache, int64_t t_cap, void* h_out, tread_stream_t stream);
 
 /* y[m, n] = linear(bf16(bf16(silu(g)) * u)) for gate_up [m, 2 inter] = [g | u], m <= 8 (silu_mul's
  * bits fused into the down projection of a decoding step, transformers Qwen2MLP). ws: at least

@@ -254,6 +254,49 @@ def test_skinny_norm_linear_equals_norm_then_linear(m, H, n, with_delta, bias):
     assert torch.equal(y, _hip.skinny_linear(x, W, b))
 
 
+@pytest.mark.parametrize("m,H,hq,hkv,hd,bias", [
+    (1, 3584, 28, 4, 128, True),    # 7B decoding step: 32-feature tiles
+    (2, 3584, 28, 4, 128, True),
+    (1, 896, 14, 2, 64, True),      # 0.5B: 16-feature tiles (36 tiles of 32 would be too few)
+    (1, 8192, 64, 8, 128, False),   # 70B, no q|k|v bias
+    (3, 512, 8, 2, 64, False),
+])
+def test_skinny_norm_qkv_rope_equals_norm_linear_then_rope_splice(m, H, hq, hkv, hd, bias):
+    """The fused q|k|v epilogue (paired feature tiles, RoPE, cache splice) gives the bits of
+    skinny_norm_linear followed by qkv_rope_splice: q, both cache layers (including the untouched
+    rows and a row index outside the cache, which splices nothing) and h + delta."""
+    g = torch.Generator().manual_seed(m * 31 + H + hq)
+    n = (hq + 2 * hkv) * hd
+    t_cap = 64
+    h = torch.randn(m, H, generator=g).to(torch.bfloat16).to(DEV)
+    d = torch.randn(m, H, generator=g).to(torch.bfloat16).to(DEV)
+    lnw = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(DEV)
+    W = (0.05 * torch.randn(n, H, generator=g)).to(torch.bfloat16).to(DEV)
+    b = torch.randn(n, generator=g).to(torch.bfloat16).to(DEV) if bias else None
+    pos = torch.tensor([5, 40, 63][:m], dtype=torch.int64, device=DEV)
+    rows = pos.clone()
+    if m == 3:
+        rows[1] = t_cap + 7  # outside the cache: its k/v are not written
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).to(DEV)
+    cos, sin = _hip.rope_table(pos, inv_freq, hd)
+    K0 = torch.randn(1, hkv, t_cap, hd, generator=g).to(torch.bfloat16).to(DEV)
+    V0 = torch.randn(1, hkv, t_cap, hd, generator=g).to(torch.bfloat16).to(DEV)
+    # two steps
+    qkv, hs_ref = _hip.skinny_norm_linear(h, d, lnw, 1e-6, W, b)
+    q_ref = torch.empty(m, hq, hd, dtype=torch.bfloat16, device=DEV)
+    K_ref, V_ref = K0.clone(), V0.clone()
+    _hip.qkv_rope_splice(qkv, cos, sin, rows, hq, hkv, hd, K_ref, V_ref, q_out=q_ref)
+    # one launch
+    q = torch.full((m, hq, hd), 9.0, dtype=torch.bfloat16, device=DEV)
+    K, V = K0.clone(), V0.clone()
+    hs = _hip.skinny_norm_qkv_rope(h, d, lnw, 1e-6, W, b, hq, hkv, hd, cos, sin, rows, q, K, V)
+    torch.cuda.synchronize()
+    assert torch.equal(hs, hs_ref)
+    assert torch.equal(q, q_ref)
+    assert torch.equal(K, K_ref) and torch.equal(V, V_ref)
+    assert not torch.equal(K, K0)  # the in-range rows were written
+
+
 @pytest.mark.parametrize("m,inter,n", [(1, 18944, 3584), (8, 512, 256), (2, 4096, 64)])
 def test_skinny_silu_linear_equals_silu_mul_then_linear(m, inter, n):
     g = torch.Generator().manual_seed(m + inter)
@@ -407,6 +450,15 @@ CASES = [
     (14, 2, 64, 9000, 5, "query"),
     (28, 4, 128, 6000, 40, "subset"),
     (64, 8, 128, 33000, 17, "query"),
+    # at most 32 rows per KV head (decoding steps): decode_attn_kernel, the keys split between the
+    # waves of a work group and across work groups (slices merged by the combine kernels), or one
+    # slice written directly
+    (28, 4, 128, 32098, 1, "query"),   # 7B step over a 32k cache: 63 slices
+    (14, 2, 64, 8100, 1, "query"),     # 0.5B step: 16 slices (few-slice merge)
+    (64, 8, 128, 33000, 4, "query"),   # 70B, 4 tokens x 8 heads = 32 rows
+    (28, 4, 128, 300, 2, "query"),     # one slice: normalised output written directly
+    (6, 3, 64, 900, 5, "subset"),      # rows scattered over the cache: per-row key ends mid-tile
+    (8, 2, 128, 2000, 4, "segfew"),    # block-diagonal visibility on a few rows
 ]
 
 
@@ -427,6 +479,10 @@ def test_subset_attention_vs_textbook(hq, hkv, hd, t_cap, n, kind):
         kend = torch.arange(n)
     elif kind == "query":  # the query rows at the end of the cache
         kend = torch.arange(t_cap - n, t_cap)
+    elif kind == "segfew":  # a few rows of packed docs: shared prefix + own segment
+        n_shared = 40
+        kend = torch.tensor([60, 300, 1210, 1999])[:n]
+        kseg = torch.tensor([40, 250, 700, 1990])[:n]
     else:  # packed docs on a shared prefix: block-diagonal visibility
         n_shared = 40
         lens = [100, 37, n - 137]

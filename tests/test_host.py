@@ -57,6 +57,9 @@ def test_error_paths_are_reported_without_a_gpu():
     # of the row tiles otherwise: 6 400 rows x 7 heads = 175 row tiles per KV head, 44 of them
     # split: 2 halves x 4 KV heads x 44 x 256 rows x (128 fp32 + max, sum) + alignment
     assert lib.tread_subset_attn_workspace_bytes(32, 28, 4, 128, 32096) > 0
+    # one decoding row of a 7B model over 32 096 keys: 63 slices of 512 keys x 4 KV heads x 32 rows
+    assert lib.tread_subset_attn_workspace_bytes(1, 28, 4, 128, 32096) == 63 * 4 * 32 * (128 * 4 + 8) + 256
+    assert lib.tread_subset_attn_workspace_bytes(2, 28, 4, 128, 300) == 0  # one slice: no partials
     assert lib.tread_subset_attn_workspace_bytes(6400, 28, 4, 128, 32096) == 2 * 4 * 44 * 256 * (128 * 4 + 8) + 256
     assert lib.tread_subset_attn_workspace_bytes(64, 28, 4, 128, 200) == 0  # 2 row tiles: neither
     assert lib.tread_subset_attn_workspace_bytes(32000, 28, 4, 128, 32096) == 0  # 3 500 work groups: balanced

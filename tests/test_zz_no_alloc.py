@@ -1,8 +1,9 @@
 """The attention entry point that allocates nothing (tread_subset_attn_scratch_bf16), through the
 C-ABI: on two calls in a row, the second with a smaller input, it gives the same bits as
 tread_subset_attn_bf16 with a workspace of its own, on the shapes whose plans use the partials
-(key halves of the recompute rows, key splits of the query rows; head_dim 128 and 64). A shape
-whose partials exceed the static array is refused with a message before anything is launched.
+(key halves of the recompute rows, key splits of the query rows, key slices of a decoding step;
+head_dim 128 and 64). A shape whose partials exceed the static array is refused with a message
+before anything is launched.
 """
 import pytest
 import torch
@@ -41,6 +42,8 @@ def _both(q, K, V, kend, hq, hkv, hd):
     ((6432, 28, 4, 128, 32096, True), (32, 28, 4, 128, 32096, False)),
     # 0.5B recompute rows (head_dim 64, key splits), then fewer rows over a shorter cache
     ((1632, 14, 2, 64, 8096, True), (200, 14, 2, 64, 3000, True)),
+    # a 7B decoding step (one row, keys split between waves and slices), then a 0.5B one
+    ((1, 28, 4, 128, 32096, False), (1, 14, 2, 64, 8096, False)),
 ])
 def test_scratch_entry_point_equals_workspace_entry_point(first, second):
     for i, (n, hq, hkv, hd, t_cap, srt) in enumerate((first, second)):

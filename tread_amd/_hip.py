@@ -10,7 +10,7 @@ from pathlib import Path
 import torch  # loads torch's HIP runtime first, so the library below binds to the same one
 
 LIB_PATH = Path(__file__).resolve().with_name("libtread_hip.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 c_i64, c_int, c_void, c_float, c_size = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
 P_I64 = ctypes.POINTER(ctypes.c_int64)
@@ -46,6 +46,9 @@ _SIGS = {
                                          c_size, c_void]),
     "tread_skinny_norm_linear_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_i64, c_i64, c_void, c_void,
                                               c_void, c_void, c_void]),
+    "tread_skinny_norm_qkv_rope_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_i64, c_void, c_void, c_int,
+                                                c_int, c_int, c_void, c_void, c_void, c_void, c_void, c_void, c_i64,
+                                                c_void, c_void]),
     "tread_skinny_silu_workspace_bytes": (c_size, [c_i64, c_i64, c_i64]),
     "tread_skinny_silu_linear_bf16": (c_int, [c_void, c_i64, c_i64, c_void, c_i64, c_void, c_void, c_size, c_void]),
     "tread_copy_async": (c_int, [c_void, c_void, c_size, c_void, c_void]),
@@ -273,6 +276,34 @@ def skinny_norm_linear(h, delta, ln_w, eps, weight, bias=None):
         _ptr(h), _ptr(delta), _ptr(ln_w), float(eps), m, n, k, _ptr(weight), _ptr(bias), _ptr(y), _ptr(h_out),
         _stream()))
     return y, (h_out if h_out is not None else h)
+
+
+def skinny_norm_qkv_rope(h, delta, ln_w, eps, wqkv, bqkv, hq, hkv, hd, cos, sin, rows, q_out, k_cache, v_cache):
+    """skinny_norm_linear of the q|k|v projection and qkv_rope_splice in one launch: q (rotated)
+    into q_out [m, hq, hd], k (rotated) and v into rows `rows` of one layer's k_cache / v_cache
+    [(1,) hkv, t_cap, hd]. Returns h + delta (h itself when delta is None); the same bits as the two
+    calls."""
+    for t, name in ((h, "h"), (wqkv, "wqkv"), (ln_w, "ln_w"), (cos, "cos"), (sin, "sin"), (q_out, "q_out"),
+                    (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _need(t, name)
+    _need(rows, "rows", torch.int64)
+    if delta is not None:
+        _need(delta, "delta")
+    if bqkv is not None:
+        _need(bqkv, "bqkv")
+    m, k = h.shape
+    n = (hq + 2 * hkv) * hd
+    t_cap = k_cache.shape[-2]
+    if (wqkv.shape != (n, k) or not norm_fused_ok(m, n, k) or (delta is not None and delta.shape != h.shape)
+            or rows.numel() != m or q_out.numel() != m * hq * hd or k_cache.shape[-3] != hkv
+            or k_cache.shape[-1] != hd or v_cache.shape != k_cache.shape or cos.shape != (m, hd // 2)
+            or sin.shape != cos.shape):
+        raise ValueError(f"skinny_norm_qkv_rope: unsupported shapes h {tuple(h.shape)} wqkv {tuple(wqkv.shape)}")
+    h_out = torch.empty_like(h) if delta is not None else None
+    _check("tread_skinny_norm_qkv_rope_bf16", lib().tread_skinny_norm_qkv_rope_bf16(
+        _ptr(h), _ptr(delta), _ptr(ln_w), float(eps), m, k, _ptr(wqkv), _ptr(bqkv), hq, hkv, hd, _ptr(cos),
+        _ptr(sin), _ptr(rows), _ptr(q_out), _ptr(k_cache), _ptr(v_cache), t_cap, _ptr(h_out), _stream()))
+    return h_out if h_out is not None else h
 
 
 def skinny_silu_linear(gate_up, weight):

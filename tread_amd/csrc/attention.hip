@@ -65,6 +65,7 @@ struct AttnArgs {
   int32_t nsplit;
   int32_t split_len;  // keys per split (multiple of ATT_BK)
   int32_t nlong;      // (nsplit 1) the nlong longest row tiles per KV head run as two work groups
+  int32_t prow;       // rows per row tile in the split-K partials (ATT_BM; DEC_ROWS for decode_attn)
   float scale_log2;
 };
 
@@ -649,6 +650,287 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     }
 }
 
+// (d) A few query rows against a long cache (decoding steps). One work group per (key slice, KV
+// head) holds every row of the launch (query tokens x the G query heads of the KV head, at most
+// DEC_ROWS: one MFMA column block) and splits the slice's keys between its waves instead of its
+// rows: wave w takes the slice's 32-key tiles w, w + 8, ..., each into its own 16 KB of LDS (K rows
+// then V rows, swizzled as in subset_attn_kernel), computes S^T = K Q^T and O^T += V^T P^T with the
+// same MFMA layouts on one 32-key block, and keeps its own running max and sums. No wave waits for
+// another inside the loop: a wave queues its next K tile as soon as its score MFMAs have read this
+// one, and its next V tile after its PV MFMAs, so its loads overlap its own arithmetic and the
+// other wave of its SIMD; its first K tile is queued before the rows' key ends are even read. At
+// the end the 8 waves' (max, sum, O) meet in LDS; one partial per row
+// goes to the split-K workspace for the combine kernels, or, with a single slice, the normalised
+// output is written directly.
+constexpr int DEC_WAVES = 8;
+constexpr int DEC_THREADS = DEC_WAVES * 64;
+constexpr int DEC_BK = 32;    // keys per wave tile
+constexpr int DEC_ROWS = 32;  // rows per launch and KV head
+
+template <int HD>
+__global__ __launch_bounds__(DEC_THREADS) void decode_attn_kernel(const AttnArgs a) {
+  using SM = AttnSmem<HD>;
+  constexpr int KS = HD / 16;            // k-steps of the score product
+  constexpr int DB = HD / 32;            // 32-row d blocks of O^T
+  constexpr int KCH = HD / 8;            // 16-byte chunks per K/V row
+  constexpr int TE = DEC_BK * HD;        // elements of one K (or V) tile
+  constexpr int LPK = TE / 8 / 64;       // 16-byte loads per lane for one K (or V) tile
+  constexpr int NV = 2 * DB;             // transposing reads per PV k-step
+  constexpr int RING = KS < 4 ? KS : 4;  // K fragment reads in flight ahead of the MFMAs
+  // per wave [K tile | V tile] while the tiles stream; the 8 waves' fp32 O rows for the merge after
+  extern __shared__ __align__(16) bf16_t smem[];
+  __shared__ float mrg_m[DEC_WAVES][DEC_ROWS], mrg_l[DEC_WAVES][DEC_ROWS];
+
+  const int split = blockIdx.x, head = blockIdx.y;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int c = lane & 31, half = lane >> 5;
+  const int k_lo = split * a.split_len;
+  bf16_t* const kbuf = smem + wv * 2 * TE;
+  bf16_t* const vbuf = kbuf + TE;
+  const bf16_t* kbase = a.k + (int64_t)head * a.t_cap * HD;
+  const bf16_t* vbase = a.v + (int64_t)head * a.t_cap * HD;
+  // Load x of a tile fills LDS chunk positions [x * 64, x * 64 + 64) of the wave's tile, lane l
+  // position x * 64 + l, with the global chunk the swizzle places there; rows from k1 on re-read
+  // row k1 - 1.
+  auto issue = [&](int k0, int k1, const bf16_t* base, bf16_t* buf, bool is_v) {
+#pragma unroll
+    for (int x = 0; x < LPK; ++x) {
+      const int pos = x * 64 + lane, row = pos / KCH, ch = pos % KCH;
+      const int sw = is_v ? SM::v_swz(row) : SM::k_swz(row);
+      const int64_t grow = min(k0 + row, k1 - 1);
+      lds_load16(base + grow * HD + (ch ^ sw) * 8, buf + x * 64 * 8);
+    }
+  };
+  // The K rows of the wave's first tile are queued before the rows' key ends are read: bounded by
+  // the slice and the cache only (finite data; keys past a row's end are masked from the scores, so
+  // they never reach P V). V rows are only read up to the last visible key.
+  {
+    const int k0 = k_lo + wv * DEC_BK, k1 = min(min(k0 + DEC_BK, k_lo + a.split_len), (int)a.t_cap);
+    if (k0 < k1) issue(k0, k1, kbase, kbuf, false);
+  }
+  const int64_t R = a.n * a.G;
+  const bool valid = c < R;  // this lane's query column: row c = (token c / G, head head * G + c % G)
+  const int64_t qi = valid ? c / a.G : 0;
+  const int qh = head * a.G + (int)(valid ? c % a.G : 0);
+  const int n_shared = a.kseg ? (int)min<int64_t>(a.n_shared, a.t_cap) : 0;
+  int my_end = -1, my_seg = 0;
+  if (valid) {
+    my_end = (int)min<int64_t>(max<int64_t>(a.kend[qi], -1), a.t_cap - 1);
+    if (a.kseg) my_seg = (int)min<int64_t>(max<int64_t>(a.kseg[qi], 0), a.t_cap);
+  }
+  // every wave holds the same rows, so wave reductions give the work group's key bounds
+  const int kmax = wave_max(my_end);
+  const int kmin = wave_min(valid ? my_end : 0x7fffffff);
+  const int segmax = wave_max(valid && a.kseg ? my_seg : 0);
+  const int k_hi = min(k_lo + a.split_len, kmax + 1);
+  const int ntiles = k_hi > k_lo ? (k_hi - k_lo + DEC_BK - 1) / DEC_BK : 0;
+
+  // Q^T fragments (B operand), pre-multiplied by scale * log2(e) and rounded to bf16, as in
+  // subset_attn_kernel
+  bf16x8_t qf[KS];
+  {
+    const bf16_t* qp = a.q + (qi * a.hq + qh) * HD + half * 8;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4_t t = {0, 0, 0, 0};
+      if (valid) t = *reinterpret_cast<const u32x4_t*>(qp + s * 16);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) t[w] = pack_bf(lo_bf(t[w]) * a.scale_log2, hi_bf(t[w]) * a.scale_log2);
+      qf[s] = __builtin_bit_cast(bf16x8_t, t);
+    }
+  }
+
+  auto tile_keys = [&](int j, int& k0, int& k1) {
+    k0 = k_lo + j * DEC_BK;
+    k1 = min(k0 + DEC_BK, k_hi);
+  };
+
+  // K fragment addresses (A operand of the score product): row c, chunk 2 s + half, swizzled
+  uint32_t kaddr[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) kaddr[s] = lds_addr(kbuf + c * HD + ((2 * s + half) ^ SM::k_swz(c)) * 8);
+  // V^T fragment addresses (transposing reads), as in subset_attn_kernel
+  uint32_t vaddr[DB];
+  {
+    const int tr_g = lane >> 4, tr_j = lane & 15;
+    const int tr_row = half * 4 + (tr_j >> 2);
+    const int tr_col = (tr_g & 1) * 16 + (tr_j & 3) * 4;
+    const int tr_swz = SM::v_swz(tr_row);
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const int col = d * 32 + tr_col;
+      vaddr[d] = lds_addr(vbuf + tr_row * HD + (((col >> 3) ^ tr_swz) << 3) + (col & 7));
+    }
+  }
+  auto v_read = [&](auto st_c, s16x4_t (&f)[NV]) {
+    constexpr int ST = decltype(st_c)::value;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      f[2 * d] = tr_read<ST * 16 * HD * 2>(vaddr[d]);
+      f[2 * d + 1] = tr_read<(ST * 16 + 8) * HD * 2>(vaddr[d]);
+    }
+  };
+
+  f32x16_t oacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int x = 0; x < 16; ++x) oacc[d][x] = 0.f;
+  float m_run = -INFINITY;  // log2-scaled running max of this lane's row (-inf: nothing visible yet)
+  float lsum[4] = {0.f, 0.f, 0.f, 0.f};
+
+  int j = wv;
+  if (j < ntiles) {
+    int k0, k1;
+    tile_keys(j, k0, k1);
+    issue(k0, k1, vbase, vbuf, true);
+  }
+  for (; j < ntiles; j += DEC_WAVES) {
+    const int jn = j + DEC_WAVES;
+    const bool more = jn < ntiles;
+    vm_wait<LPK>();  // this tile's K landed (its V may still fly)
+    // S^T = K Q^T: register x of sc holds key (x / 4) * 8 + half * 4 + x % 4 of the tile
+    f32x16_t sc;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) sc[x] = 0.f;
+    {
+      bf16x8_t kf[KS];
+      static_for<RING>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        kf[i] = lds_read128<0>(kaddr[i]);
+      });
+      static_for<KS>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        constexpr int k_after = (i + RING - 1 < KS - 1 ? i + RING - 1 : KS - 1) - i;
+        lgkm_wait<k_after>(kf[i]);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i], qf[i], sc, 0, 0, 0);
+        if constexpr (i + RING < KS) kf[i + RING] = lds_read128<0>(kaddr[i + RING]);
+      });
+    }
+    if (more) {  // every K fragment read has completed
+      int n0, n1;
+      tile_keys(jn, n0, n1);
+      issue(n0, n1, kbase, kbuf, false);
+    }
+    int k0, k1;
+    tile_keys(j, k0, k1);
+    const bool full = (k1 - k0 == DEC_BK) && (k1 - 1 <= kmin) && (k0 >= segmax || k1 <= n_shared || !a.kseg);
+    if (!full) {
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        const int key = k0 + (x >> 2) * 8 + half * 4 + (x & 3);
+        const bool vis = key < k1 && key <= my_end && (!a.kseg || key < n_shared || key >= my_seg);
+        sc[x] = vis ? sc[x] : -INFINITY;
+      }
+    }
+    float mx = sc[0];
+#pragma unroll
+    for (int x = 1; x < 16; ++x) mx = fmaxf(mx, sc[x]);
+    const float m_new = fmaxf(m_run, xhalf_max(mx));
+    const bool any = m_new > -INFINITY;
+    const float corr = any ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+    const float msub = any ? m_new : 0.f;
+    m_run = m_new;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) lsum[q4] *= corr;
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) oacc[d][x] *= corr;
+    bf16x8_t pb[2];
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const float p = __builtin_amdgcn_exp2f(sc[x] - msub);
+      sc[x] = p;
+      lsum[x & 3] += p;
+    }
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      u32x4_t pw;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) pw[q4] = pack_bf(sc[h2 * 8 + 2 * q4], sc[h2 * 8 + 2 * q4 + 1]);
+      pb[h2] = __builtin_bit_cast(bf16x8_t, pw);
+    }
+    // this tile's V landed (the next K tile may still fly)
+    if (more) vm_wait<LPK>();
+    else vm_wait<0>();
+    // O^T += V^T P^T: k-step st covers tile keys st * 16 + half * 4 + (0..3) and st * 16 + 8 + half * 4 + (0..3)
+    {
+      s16x4_t v0[NV], v1[NV];
+      v_read(std::integral_constant<int, 0>{}, v0);
+      v_read(std::integral_constant<int, 1>{}, v1);
+      auto mm = [&](const s16x4_t (&f)[NV], const bf16x8_t& p) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+          const bf16x8_t va = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(f[2 * d], f[2 * d + 1], 0, 1, 2, 3, 4, 5, 6, 7));
+          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, p, oacc[d], 0, 0, 0);
+        }
+      };
+      lgkm_wait<NV>(v0);
+      mm(v0, pb[0]);
+      lgkm_wait<0>(v1);
+      mm(v1, pb[1]);
+    }
+    if (more) {  // every V fragment read has completed
+      int n0, n1;
+      tile_keys(jn, n0, n1);
+      issue(n0, n1, vbase, vbuf, true);
+    }
+  }
+  vm_wait<0>();  // a first K tile queued for a wave without tiles lands before its LDS is reused
+
+  // ---- merge the 8 waves' partials of each row
+  const float l_row = xhalf_sum((lsum[0] + lsum[1]) + (lsum[2] + lsum[3]));
+  __syncthreads();  // every wave is done with its tile buffers
+  float* const mo = reinterpret_cast<float*>(smem);  // [wave][row][HD]
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const f32x4_t o = {oacc[d][g4 * 4 + 0], oacc[d][g4 * 4 + 1], oacc[d][g4 * 4 + 2], oacc[d][g4 * 4 + 3]};
+      *reinterpret_cast<f32x4_t*>(mo + (wv * DEC_ROWS + c) * HD + d * 32 + g4 * 8 + half * 4) = o;
+    }
+  if (half == 0) {
+    mrg_m[wv][c] = m_run;
+    mrg_l[wv][c] = l_row;
+  }
+  __syncthreads();
+  constexpr int DQ = HD / 4;
+  for (int it = threadIdx.x; it < DEC_ROWS * DQ; it += DEC_THREADS) {
+    const int rr = it / DQ, dq = it % DQ;
+    if (rr >= R) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < DEC_WAVES; ++w)
+      if (mrg_l[w][rr] > 0.f) M = fmaxf(M, mrg_m[w][rr]);
+    float L = 0.f;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < DEC_WAVES; ++w) {
+      const float l = mrg_l[w][rr];
+      if (l > 0.f) {
+        const float wgt = __builtin_amdgcn_exp2f(mrg_m[w][rr] - M);
+        L += wgt * l;
+        acc += wgt * *reinterpret_cast<const f32x4_t*>(mo + (w * DEC_ROWS + rr) * HD + dq * 4);
+      }
+    }
+    if (a.nsplit > 1) {
+      const int64_t p = ((int64_t)split * a.hkv + head) * DEC_ROWS + rr;
+      *reinterpret_cast<f32x4_t*>(a.ws_o + p * HD + dq * 4) = acc;
+      if (dq == 0) {
+        a.ws_ml[p * 2] = L > 0.f ? M : 0.f;
+        a.ws_ml[p * 2 + 1] = L;
+      }
+    } else {
+      const float inv = L > 0.f ? 1.0f / L : 0.f;
+      const int64_t qr = rr / a.G;
+      const int qhr = head * a.G + rr % a.G;
+      const u32x2_t o2 = {pack_bf(acc[0] * inv, acc[1] * inv), pack_bf(acc[2] * inv, acc[3] * inv)};
+      *reinterpret_cast<u32x2_t*>(a.out + (qr * a.hq + qhr) * HD + dq * 4) = o2;
+    }
+  }
+}
+
 // Merge split-K partials: one work group per (kv head, row). The split maxima and sums go through
 // LDS; each thread then owns 4 output elements of one split group (every SG-th split), and the
 // groups' weighted partial sums are reduced in LDS.
@@ -665,9 +947,9 @@ __global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(const AttnArg
   const int64_t w = blockIdx.x;
   const int head = (int)(w / R);
   const int64_t r = w % R;
-  const int tile = (int)(r / ATT_BM), in_tile = (int)(r % ATT_BM);
-  const int64_t stride = (int64_t)a.hkv * a.tiles * ATT_BM;
-  const int64_t p0 = ((int64_t)head * a.tiles + tile) * ATT_BM + in_tile;
+  const int tile = (int)(r / a.prow), in_tile = (int)(r % a.prow);
+  const int64_t stride = (int64_t)a.hkv * a.tiles * a.prow;
+  const int64_t p0 = ((int64_t)head * a.tiles + tile) * a.prow + in_tile;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   // global max of the split maxima
   float m = -INFINITY;
@@ -778,9 +1060,9 @@ __global__ __launch_bounds__(HALF_ROWS * 64) void attn_combine_few_kernel(const 
   if (w >= (int64_t)a.hkv * R) return;
   const int head = (int)(w / R);
   const int64_t r = w % R;
-  const int tile = (int)(r / ATT_BM), in_tile = (int)(r % ATT_BM);
-  const int64_t stride = (int64_t)a.hkv * a.tiles * ATT_BM;
-  const int64_t p0 = ((int64_t)head * a.tiles + tile) * ATT_BM + in_tile;
+  const int tile = (int)(r / a.prow), in_tile = (int)(r % a.prow);
+  const int64_t stride = (int64_t)a.hkv * a.tiles * a.prow;
+  const int64_t p0 = ((int64_t)head * a.tiles + tile) * a.prow + in_tile;
   // every slice's (max, sum) and partial O are loaded up front (one round of memory latency, not
   // one per slice); the merge then walks the slices in order
   float mv[CMB_FEW_SPLITS], lv[CMB_FEW_SPLITS], ov[CMB_FEW_SPLITS][EPL];
@@ -826,8 +1108,15 @@ __global__ __launch_bounds__(HALF_ROWS * 64) void attn_combine_few_kernel(const 
 struct SplitPlan {
   int nsplit, split_len;
   int64_t tiles;
-  int nlong;  // one work group per key half for the nlong longest row tiles of each KV head
+  int nlong;    // one work group per key half for the nlong longest row tiles of each KV head
+  bool decode;  // decode_attn_kernel: at most DEC_ROWS rows per KV head, keys split between waves
 };
+
+// Keys per decode_attn work group: at most about DEC_TARGET_WGS work groups over the cache (one
+// per CU: each holds 130 KiB of LDS, so a few more would run as a second round), in whole 32-key
+// tiles, at least two tiles per wave, and at most CMB_MAX_SPLITS slices.
+constexpr int DEC_TARGET_WGS = 256;
+constexpr int DEC_MIN_SPLIT = 2 * DEC_WAVES * DEC_BK;
 
 // Row tiles per KV head run as two half-range work groups when there is no key split and the
 // launch is a few rounds of the GPU: a quarter of them (the longest). Simulated dispatch of the
@@ -842,6 +1131,20 @@ constexpr int64_t ATT_LONG_MAX_WGS = 1536;
 
 static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
   SplitPlan sp;
+  sp.decode = false;
+  if (n * (hq / hkv) <= DEC_ROWS) {
+    sp.decode = true;
+    sp.tiles = 1;
+    sp.nlong = 0;
+    const int64_t unit = DEC_BK;  // whole tiles; the waves take them round-robin
+    int64_t len = (t_cap * hkv + DEC_TARGET_WGS - 1) / DEC_TARGET_WGS;
+    if (len < DEC_MIN_SPLIT) len = DEC_MIN_SPLIT;
+    if (len < (t_cap + CMB_MAX_SPLITS - 1) / CMB_MAX_SPLITS) len = (t_cap + CMB_MAX_SPLITS - 1) / CMB_MAX_SPLITS;
+    len = (len + unit - 1) / unit * unit;
+    sp.nsplit = (int)((t_cap + len - 1) / len);
+    sp.split_len = (int)len;
+    return sp;
+  }
   sp.tiles = (n * (hq / hkv) + ATT_BM - 1) / ATT_BM;
   const int64_t base = (int64_t)hkv * sp.tiles;
   sp.nsplit = 1;
@@ -869,6 +1172,7 @@ static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
 }
 
 static size_t split_rows(const SplitPlan& sp, int hkv) {
+  if (sp.decode) return sp.nsplit > 1 ? (size_t)sp.nsplit * hkv * DEC_ROWS : 0;
   if (sp.nsplit > 1) return (size_t)sp.nsplit * hkv * sp.tiles * ATT_BM;
   return (size_t)2 * hkv * sp.nlong * ATT_BM;
 }
@@ -885,6 +1189,39 @@ using namespace tread;
 static int subset_attn_impl(const void* q, const void* k_cache, const void* v_cache, const int64_t* kend,
                             const int64_t* kseg, int64_t n_shared, int64_t n, int hq, int hkv, int head_dim,
                             int64_t t_cap, float scale, void* out, void* ws, size_t ws_bytes, tread_stream_t stream);
+
+// Merge the a.nsplit key-slice partials of every row (one work group, or with few slices one wave,
+// per (KV head, row)).
+static int launch_combine(const AttnArgs& a, int head_dim, hipStream_t s) {
+  const int64_t blocks = (int64_t)a.hkv * a.n * a.G;
+  if (a.nsplit <= CMB_FEW_SPLITS) {
+    const dim3 fgrid((unsigned)((blocks + HALF_ROWS - 1) / HALF_ROWS));
+    if (head_dim == 128)
+      hipLaunchKernelGGL(attn_combine_few_kernel<128>, fgrid, dim3(HALF_ROWS * 64), 0, s, a);
+    else
+      hipLaunchKernelGGL(attn_combine_few_kernel<64>, fgrid, dim3(HALF_ROWS * 64), 0, s, a);
+    return check_launch("subset_attn combine");
+  }
+  if (head_dim == 128)
+    hipLaunchKernelGGL(attn_combine_kernel<128>, dim3((unsigned)blocks), dim3(CMB_THREADS), 0, s, a);
+  else
+    hipLaunchKernelGGL(attn_combine_kernel<64>, dim3((unsigned)blocks), dim3(CMB_THREADS), 0, s, a);
+  return check_launch("subset_attn combine");
+}
+
+// decode_attn_kernel over (key slice, KV head) work groups, then the slice merge (nsplit > 1).
+static int decode_attn_launch(AttnArgs& a, const SplitPlan& sp, int head_dim, hipStream_t s) {
+  a.prow = DEC_ROWS;
+  const dim3 grid((unsigned)sp.nsplit, (unsigned)a.hkv);
+  const size_t smem = (size_t)DEC_WAVES * DEC_ROWS * head_dim * sizeof(float);  // = 8 waves' K and V tiles
+  if (head_dim == 128)
+    hipLaunchKernelGGL(decode_attn_kernel<128>, grid, dim3(DEC_THREADS), smem, s, a);
+  else
+    hipLaunchKernelGGL(decode_attn_kernel<64>, grid, dim3(DEC_THREADS), smem, s, a);
+  int rc = check_launch("subset_attn decode");
+  if (rc || sp.nsplit <= 1) return rc;
+  return launch_combine(a, head_dim, s);
+}
 
 extern "C" size_t tread_subset_attn_workspace_bytes(int64_t n, int hq, int hkv, int head_dim, int64_t t_cap) {
   if (n <= 0 || hq <= 0 || hkv <= 0 || (hq % hkv) != 0 || t_cap <= 0) return 0;
@@ -985,9 +1322,10 @@ static int subset_attn_impl(const void* q, const void* k_cache, const void* v_ca
   a.G = hq / hkv;
   SplitPlan sp = plan_split(n, hq, hkv, t_cap);
   const size_t need = split_ws_bytes(sp, hkv, head_dim);
-  if (need && (!ws || ws_bytes < need)) {  // no workspace: one pass per row tile
+  if (need && (!ws || ws_bytes < need)) {  // no workspace: one pass per row tile (decode: one slice)
     sp.nsplit = 1;
     sp.nlong = 0;
+    if (sp.decode) sp.split_len = (int)((t_cap + DEC_WAVES * DEC_BK - 1) / (DEC_WAVES * DEC_BK) * (DEC_WAVES * DEC_BK));
   }
   const int64_t vtiles = sp.tiles + sp.nlong;  // work groups per KV head without a key split
   if (vtiles > 0x7fffffffLL / N_XCD) return fail(TREAD_ERANGE, "subset_attn: too many rows");
@@ -1001,6 +1339,8 @@ static int subset_attn_impl(const void* q, const void* k_cache, const void* v_ca
     a.ws_o = a.ws_ml + split_rows(sp, hkv) * 2;
   }
   a.scale_log2 = scale * 1.4426950408889634f;
+  if (sp.decode) return decode_attn_launch(a, sp, head_dim, (hipStream_t)stream);
+  a.prow = ATT_BM;
   int64_t grid;
   if (sp.nsplit > 1) {
     a.xpg = 0;
@@ -1031,18 +1371,5 @@ static int subset_attn_impl(const void* q, const void* k_cache, const void* v_ca
     return check_launch("subset_attn halves");
   }
   if (sp.nsplit <= 1) return rc;
-  const int64_t blocks = (int64_t)hkv * n * a.G;
-  if (sp.nsplit <= CMB_FEW_SPLITS) {
-    const dim3 fgrid((unsigned)((blocks + HALF_ROWS - 1) / HALF_ROWS));
-    if (head_dim == 128)
-      hipLaunchKernelGGL(attn_combine_few_kernel<128>, fgrid, dim3(HALF_ROWS * 64), 0, s, a);
-    else
-      hipLaunchKernelGGL(attn_combine_few_kernel<64>, fgrid, dim3(HALF_ROWS * 64), 0, s, a);
-    return check_launch("subset_attn combine");
-  }
-  if (head_dim == 128)
-    hipLaunchKernelGGL(attn_combine_kernel<128>, dim3((unsigned)blocks), dim3(CMB_THREADS), 0, s, a);
-  else
-    hipLaunchKernelGGL(attn_combine_kernel<64>, dim3((unsigned)blocks), dim3(CMB_THREADS), 0, s, a);
-  return check_launch("subset_attn combine");
+  return launch_combine(a, head_dim, s);
 }

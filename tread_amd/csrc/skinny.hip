@@ -37,14 +37,30 @@ struct SkinnyArgs {
   int64_t ldy;
   float* part;
   int M, K, N;
+  // EPI_ROPE: q|k|v of a decoder layer (N = (hq + 2 hkv) hd): q and k rotated (cos / sin [M, hd / 2])
+  // into q_out [M, hq, hd] and k_cache, v into v_cache, row rows[m] of each [hkv, t_cap, hd] cache
+  const bf16_t* cosb;
+  const bf16_t* sinb;
+  const int64_t* rows;
+  bf16_t* q_out;
+  bf16_t* k_cache;
+  bf16_t* v_cache;
+  int64_t t_cap;
+  int hq, hkv, hd;
 };
+
+enum { EPI_PLAIN = 0, EPI_ROPE = 1 };
 
 // blockIdx.y = q selects the K slice [q K / ks, (q + 1) K / ks); with ks > 1 the slice's fp32 sums
 // go to part[q][m][n] and skinny_reduce_kernel finishes them.
 // PRO_NORM stages norm(h + delta) of the M rows in LDS first (add_rmsnorm_row: the same bits as
 // the stand-alone add + RMSNorm kernel) and work group (0, 0) writes h + delta to h_out; PRO_SILU
 // stages this work group's K slice of bf16(bf16(silu(g)) * u) (the same bits as silu_mul_kernel).
-template <int PRO, int CPT, int TN>
+// EPI_ROPE (with PRO_NORM, unsplit): a q or k head's tile p holds the feature pairs (d, d + hd / 2)
+// for d in [p TN / 2, (p + 1) TN / 2), so that the epilogue rotates each pair in place with the
+// rounding points of qkv_rope_splice_kernel (transformers' apply_rotary_pos_emb in bf16) and writes
+// q and the cache rows itself; v heads keep their features in order.
+template <int PRO, int CPT, int TN, int EPI = EPI_PLAIN>
 __global__ __launch_bounds__(SK_WAVES * 64) void skinny_gemm_kernel(const SkinnyArgs a) {
   static_assert(TN == 32 || TN == 16, "tile of 32 or 16 features");
   constexpr int KSTEP = 512 / TN;     // K per MFMA: 16 (32 x 32 x 16) or 32 (16 x 16 x 32)
@@ -61,7 +77,14 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_gemm_kernel(const Skinny
   const int kslice = K / ks, k0 = q * kslice;
   const int kw = kslice / SK_WAVES;  // a multiple of KSTEP
   const int kb = k0 + wv * kw + kg * 8;  // this lane's first K
-  const bf16_t* wp = a.w + (n0 + rt) * (int64_t)K + kb;
+  // weight row of tile row rt
+  int64_t wrow = n0 + rt;
+  if constexpr (EPI == EPI_ROPE) {
+    const int tph = a.hd / TN, hh = blockIdx.x / tph, p = blockIdx.x % tph;
+    if (hh < a.hq + a.hkv)
+      wrow = (int64_t)hh * a.hd + (rt < TN / 2 ? p * (TN / 2) + rt : a.hd / 2 + p * (TN / 2) + rt - TN / 2);
+  }
+  const bf16_t* wp = a.w + wrow * (int64_t)K + kb;
   const bool xon = rt < M;
   const int xrow = xon ? rt : 0;
   const u32x4_t zero = {0u, 0u, 0u, 0u};
@@ -123,13 +146,55 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_gemm_kernel(const Skinny
   __syncthreads();
   // C layout: lane l holds column (token) l % TN; register r holds row (r / 4) * 8 + (l / 32) * 4 + r % 4
   // of the 32 x 32 tile, row (l / 16) * 4 + r of the 16 x 16 tile
-  for (int t = threadIdx.x; t < TN * M; t += SK_WAVES * 64) {
-    const int m = t / TN, row = t % TN;
+  auto tile_sum = [&](int m, int row) {
     const int r = TN == 32 ? (row >> 3) * 4 + (row & 3) : (row & 3);
     const int ln = TN == 32 ? m + 32 * ((row >> 2) & 1) : m + 16 * (row >> 2);
     float v = 0.f;
 #pragma unroll
     for (int p = 0; p < SK_WAVES; ++p) v += red[p][r][ln];
+    return v;
+  };
+  if constexpr (EPI == EPI_ROPE) {
+    const int tph = a.hd / TN, hh = blockIdx.x / tph, p = blockIdx.x % tph, half_hd = a.hd / 2;
+    if (hh < a.hq + a.hkv) {  // q or k: rotate each (d, d + hd / 2) pair
+      for (int t = threadIdx.x; t < (TN / 2) * M; t += SK_WAVES * 64) {
+        const int m = t / (TN / 2), pr = t % (TN / 2), d = p * (TN / 2) + pr;
+        const int64_t f = (int64_t)hh * a.hd + d;
+        float lo = tile_sum(m, pr), hi = tile_sum(m, pr + TN / 2);
+        if (a.bias) {
+          lo += bf2f(a.bias[f]);
+          hi += bf2f(a.bias[f + half_hd]);
+        }
+        const float x1 = bf2f(f2bf(lo)), x2 = bf2f(f2bf(hi));
+        const float co = bf2f(a.cosb[(int64_t)m * half_hd + d]), si = bf2f(a.sinb[(int64_t)m * half_hd + d]);
+        const bf16_t o1 = f2bf(bf2f(f2bf(x1 * co)) + bf2f(f2bf(-x2 * si)));
+        const bf16_t o2 = f2bf(bf2f(f2bf(x2 * co)) + bf2f(f2bf(x1 * si)));
+        bf16_t* dst;
+        if (hh < a.hq) {
+          dst = a.q_out + ((int64_t)m * a.hq + hh) * a.hd;
+        } else {
+          const int64_t row = a.rows[m];
+          if (row < 0 || row >= a.t_cap) continue;  // out-of-range rows splice nothing
+          dst = a.k_cache + ((int64_t)(hh - a.hq) * a.t_cap + row) * a.hd;
+        }
+        dst[d] = o1;
+        dst[d + half_hd] = o2;
+      }
+    } else {  // v: into the cache unrotated
+      for (int t = threadIdx.x; t < TN * M; t += SK_WAVES * 64) {
+        const int m = t / TN, row = t % TN;
+        const int64_t crow = a.rows[m];
+        if (crow < 0 || crow >= a.t_cap) continue;
+        float v = tile_sum(m, row);
+        if (a.bias) v += bf2f(a.bias[n0 + row]);
+        a.v_cache[((int64_t)(hh - a.hq - a.hkv) * a.t_cap + crow) * a.hd + p * TN + row] = f2bf(v);
+      }
+    }
+    return;
+  }
+  for (int t = threadIdx.x; t < TN * M; t += SK_WAVES * 64) {
+    const int m = t / TN, row = t % TN;
+    float v = tile_sum(m, row);
     if (ks > 1) {
       a.part[((int64_t)q * M + m) * a.N + n0 + row] = v;
     } else {
@@ -179,20 +244,25 @@ static int skinny_ksplit(int tn, int64_t n, int64_t k) {
 
 using namespace tread;
 
-template <int PRO, int CPT>
+template <int PRO, int CPT, int EPI = EPI_PLAIN>
 static void launch_tile(int tn, dim3 grid, size_t lds, hipStream_t s, const SkinnyArgs& a) {
-  if (tn == 16) hipLaunchKernelGGL((skinny_gemm_kernel<PRO, CPT, 16>), grid, dim3(SK_WAVES * 64), lds, s, a);
-  else hipLaunchKernelGGL((skinny_gemm_kernel<PRO, CPT, 32>), grid, dim3(SK_WAVES * 64), lds, s, a);
+  if (tn == 16) hipLaunchKernelGGL((skinny_gemm_kernel<PRO, CPT, 16, EPI>), grid, dim3(SK_WAVES * 64), lds, s, a);
+  else hipLaunchKernelGGL((skinny_gemm_kernel<PRO, CPT, 32, EPI>), grid, dim3(SK_WAVES * 64), lds, s, a);
+}
+
+template <int EPI>
+static void launch_norm(int cpt, int tn, dim3 grid, size_t lds, hipStream_t s, const SkinnyArgs& a) {
+  if (cpt <= 1) launch_tile<PRO_NORM, 1, EPI>(tn, grid, lds, s, a);
+  else if (cpt <= 2) launch_tile<PRO_NORM, 2, EPI>(tn, grid, lds, s, a);
+  else if (cpt <= 4) launch_tile<PRO_NORM, 4, EPI>(tn, grid, lds, s, a);
+  else launch_tile<PRO_NORM, 8, EPI>(tn, grid, lds, s, a);
 }
 
 static int launch_skinny(int pro, int cpt, int tn, const SkinnyArgs& a, int ks, size_t lds, hipStream_t s) {
   const dim3 grid((unsigned)(a.N / tn), (unsigned)ks);
   if (pro == PRO_NONE) launch_tile<PRO_NONE, 1>(tn, grid, lds, s, a);
   else if (pro == PRO_SILU) launch_tile<PRO_SILU, 1>(tn, grid, lds, s, a);
-  else if (cpt <= 1) launch_tile<PRO_NORM, 1>(tn, grid, lds, s, a);
-  else if (cpt <= 2) launch_tile<PRO_NORM, 2>(tn, grid, lds, s, a);
-  else if (cpt <= 4) launch_tile<PRO_NORM, 4>(tn, grid, lds, s, a);
-  else launch_tile<PRO_NORM, 8>(tn, grid, lds, s, a);
+  else launch_norm<EPI_PLAIN>(cpt, tn, grid, lds, s, a);
   int rc = check_launch("skinny_linear");
   if (rc || ks <= 1) return rc;
   const int64_t total = (int64_t)a.M * a.N;
@@ -292,6 +362,54 @@ extern "C" int tread_skinny_norm_linear_bf16(const void* h, const void* delta, c
   a.N = (int)n;
   const int nthr = rmsnorm_threads((int)k), cpt = (int)((k / 8 + nthr - 1) / nthr);
   return launch_skinny(PRO_NORM, cpt, skinny_tn(m, n, k), a, 1, (size_t)m * k * sizeof(bf16_t), (hipStream_t)stream);
+}
+
+extern "C" int tread_skinny_norm_qkv_rope_bf16(const void* h, const void* delta, const void* ln_weight, float eps,
+                                               int64_t m, int64_t hidden, const void* wqkv, const void* bqkv, int hq,
+                                               int hkv, int head_dim, const void* cos, const void* sin,
+                                               const int64_t* rows, void* q_out, void* k_cache, void* v_cache,
+                                               int64_t t_cap, void* h_out, tread_stream_t stream) {
+  if (m == 0) return 0;
+  if (hq <= 0 || hkv <= 0 || (head_dim != 64 && head_dim != 128) || t_cap <= 0)
+    return fail(TREAD_EINVAL, "skinny_norm_qkv_rope: bad heads (hq=%d hkv=%d head_dim=%d t_cap=%lld)", hq, hkv,
+                head_dim, (long long)t_cap);
+  const int64_t n = (int64_t)(hq + 2 * hkv) * head_dim;
+  if (int rc = check_shape("skinny_norm_qkv_rope", m, 8, n, hidden)) return rc;
+  if (hidden > 16384) return fail(TREAD_EINVAL, "skinny_norm_qkv_rope: hidden %lld above 16384", (long long)hidden);
+  if ((size_t)m * hidden * sizeof(bf16_t) > SK_STAGE_MAX)
+    return fail(TREAD_EINVAL, "skinny_norm_qkv_rope: %lld rows of %lld do not fit in LDS", (long long)m,
+                (long long)hidden);
+  if (!h || !ln_weight || !wqkv || !cos || !sin || !rows || !q_out || !k_cache || !v_cache)
+    return fail(TREAD_EINVAL, "skinny_norm_qkv_rope: null pointer");
+  if ((((uintptr_t)h | (uintptr_t)delta | (uintptr_t)ln_weight | (uintptr_t)wqkv | (uintptr_t)h_out) & 15) != 0)
+    return fail(TREAD_EINVAL, "skinny_norm_qkv_rope: operands not 16-byte aligned");
+  SkinnyArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = (const bf16_t*)h;
+  a.ldx = hidden;
+  a.delta = (const bf16_t*)delta;
+  a.lnw = (const bf16_t*)ln_weight;
+  a.eps = eps;
+  a.h_out = (bf16_t*)h_out;
+  a.w = (const bf16_t*)wqkv;
+  a.bias = (const bf16_t*)bqkv;
+  a.M = (int)m;
+  a.K = (int)hidden;
+  a.N = (int)n;
+  a.cosb = (const bf16_t*)cos;
+  a.sinb = (const bf16_t*)sin;
+  a.rows = rows;
+  a.q_out = (bf16_t*)q_out;
+  a.k_cache = (bf16_t*)k_cache;
+  a.v_cache = (bf16_t*)v_cache;
+  a.t_cap = t_cap;
+  a.hq = hq;
+  a.hkv = hkv;
+  a.hd = head_dim;
+  const int tn = skinny_tn(m, n, hidden);  // the tile skinny_norm_linear picks: the same sums
+  const int nthr = rmsnorm_threads((int)hidden), cpt = (int)((hidden / 8 + nthr - 1) / nthr);
+  launch_norm<EPI_ROPE>(cpt, tn, dim3((unsigned)(n / tn), 1), (size_t)m * hidden * sizeof(bf16_t), (hipStream_t)stream, a);
+  return check_launch("skinny_norm_qkv_rope");
 }
 
 extern "C" int tread_skinny_silu_linear_bf16(const void* gate_up, int64_t m, int64_t inter, const void* weight,

@@ -122,9 +122,15 @@ def _layer_few_rows(P, l, lw, h, delta, R, K, V):
     """layer_forward for a few rows: (norm ->) q|k|v, RoPE + splice, attention, o, (norm ->)
     gate|up, (SiLU ->) down, with the same roundings as the layer for many rows."""
     hq, hkv, hd = P.hq, P.hkv, P.hd
-    qkv, h = _norm_linear(P, h, delta, lw.ln1, lw.wqkv, lw.bqkv)
-    q = torch.empty(h.shape[0], hq, hd, dtype=h.dtype, device=h.device)
-    _hip.qkv_rope_splice(qkv, R.cos, R.sin, R.rows, hq, hkv, hd, K[l], V[l], q_out=q)
+    m = h.shape[0]
+    q = torch.empty(m, hq, hd, dtype=h.dtype, device=h.device)
+    if m <= NORM_FUSED_ROWS and _hip.norm_fused_ok(m, lw.wqkv.shape[0], lw.wqkv.shape[1]):
+        # norm, q|k|v, RoPE and the cache splice in one launch (the same bits as the three steps)
+        h = _hip.skinny_norm_qkv_rope(h, delta, lw.ln1, P.eps, lw.wqkv, lw.bqkv, hq, hkv, hd, R.cos, R.sin, R.rows,
+                                      q, K[l], V[l])
+    else:
+        qkv, h = _norm_linear(P, h, delta, lw.ln1, lw.wqkv, lw.bqkv)
+        _hip.qkv_rope_splice(qkv, R.cos, R.sin, R.rows, hq, hkv, hd, K[l], V[l], q_out=q)
     o = _hip.subset_attn(q, K[l], V[l], R.kend, hq, hkv, hd, P.scale, kseg=R.kseg, n_shared=R.n_shared)
     a = _hip.skinny_linear(o, lw.wo)
     gu, h = _norm_linear(P, h, a, lw.ln2, lw.wgu)
