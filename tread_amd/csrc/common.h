@@ -42,8 +42,9 @@ __host__ __device__ __forceinline__ int rmsnorm_threads(int hidden) {
 // block must call it, for its barriers): s = bf16(x + d) (d may be null; s goes to sum_row if not
 // null), out_row = bf16(w * bf16(s * r)) with r = 1 / sqrt(mean(s^2) + eps), the rounding points
 // of transformers' Qwen2RMSNorm. Thread t owns the 16-byte chunks t, t + nthr, ..., sums its
-// squares in that order, and the wave totals are added in wave order, so every caller with the
-// same nthr gets the same bits. red: 32 floats of shared memory.
+// squares in that order, and the wave totals are added in wave order (by every thread, after one
+// barrier), so every caller with the same nthr gets the same bits. The weight chunks are loaded
+// with the row's, so the row costs one round of memory latency. red: 32 floats of shared memory.
 template <int CPT>
 __device__ __forceinline__ void add_rmsnorm_row(const bf16_t* __restrict__ xr, const bf16_t* __restrict__ dr,
                                                 const bf16_t* __restrict__ w, float eps, int hidden, int nthr,
@@ -51,8 +52,13 @@ __device__ __forceinline__ void add_rmsnorm_row(const bf16_t* __restrict__ xr, c
                                                 float* red) {
   const int tid = threadIdx.x, nch = hidden / 8;
   const bool on = tid < nthr;
-  u32x4_t v[CPT];
+  u32x4_t v[CPT], ww[CPT];
   float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = tid + j * nthr;
+    if (on && c < nch) ww[j] = *reinterpret_cast<const u32x4_t*>(w + c * 8);
+  }
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
     const int c = tid + j * nthr;
@@ -77,29 +83,24 @@ __device__ __forceinline__ void add_rmsnorm_row(const bf16_t* __restrict__ xr, c
   for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
   if (on && (tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
-  if (tid == 0) {
-    float t = 0.f;
-    for (int k = 0; k < nthr / 64; ++k) t += red[k];
-    red[31] = 1.0f / sqrtf(t / (float)hidden + eps);
-  }
-  __syncthreads();
-  const float r = red[31];
+  float t = 0.f;
+  for (int k = 0; k < nthr / 64; ++k) t += red[k];
+  const float r = 1.0f / sqrtf(t / (float)hidden + eps);
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
     const int c = tid + j * nthr;
     if (on && c < nch) {
-      const u32x4_t ww = *reinterpret_cast<const u32x4_t*>(w + c * 8);
       u32x4_t o;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float l = bf2f(f2bf(lo_bf(v[j][q]) * r)) * lo_bf(ww[q]);
-        const float h = bf2f(f2bf(hi_bf(v[j][q]) * r)) * hi_bf(ww[q]);
+        const float l = bf2f(f2bf(lo_bf(v[j][q]) * r)) * lo_bf(ww[j][q]);
+        const float h = bf2f(f2bf(hi_bf(v[j][q]) * r)) * hi_bf(ww[j][q]);
         o[q] = pack_bf(l, h);
       }
       *reinterpret_cast<u32x4_t*>(out_row + c * 8) = o;
     }
   }
-  __syncthreads();  // red is reused by the next row
+  __syncthreads();  // out_row is complete for every thread, and red may be reused by the next row
 }
 
 template <typename T>

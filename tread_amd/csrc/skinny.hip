@@ -216,6 +216,177 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
   y[(int64_t)m * ldy + n] = f2bf(v);
 }
 
+// One row (a decoding step): one weight row per wave. The MFMA tiles above read 16-32 weight rows
+// per wave in 64-byte pieces, which spreads HBM traffic over tens of thousands of short streams;
+// at one row, streaming whole rows is faster on every decode shape (7B, weights from HBM, one
+// process: gate|up 52.5 -> 43.9 us, down 29.1 -> 23.8, o 11.7 -> 7.5, q|k|v 13.1 -> 8.4). A work
+// group of 8 waves stages the operand row in LDS (the same prologues as the tiles: add + RMSNorm
+// or SiLU gating, the same bits), then in each of its rpw passes every wave streams one weight row
+// (lane l takes the 16-byte chunks l, l + 64, ..., GV_U loads in flight), sums its fp32 products
+// in chunk order, reduces across the wave and adds the bias before the one rounding. EPI_ROPE: a
+// pass's 8 rows are 4 (d, d + hd/2) pairs of a q or k head, rotated together once the passes are
+// done, or 8 rows of a v head, written to the cache directly.
+constexpr int GV_WAVES = 8;
+constexpr int GV_U = 4;  // 16-byte loads in flight per lane (2: 2 % slower per step; 8 spills at 64 VGPRs)
+constexpr int GV_MAX_RPW = 8;
+
+template <int PRO, int CPT, int EPI>
+// Eight waves per SIMD (at most 64 VGPRs) unless the norm prologue holds more of the row per
+// thread: the compiler's own choice (98-108 VGPRs, four waves) left the streams too few in flight
+// (7B decoding step 3.90 -> 3.55 ms with the cap).
+__global__ __launch_bounds__(GV_WAVES * 64) __attribute__((amdgpu_waves_per_eu(CPT >= 8 ? 4 : CPT >= 4 ? 6 : 8, 8)))
+void gemv_kernel(const SkinnyArgs a, int rpw) {
+  extern __shared__ __align__(16) bf16_t xs[];  // the operand row [K]
+  __shared__ float nred[32];
+  __shared__ float sums[GV_MAX_RPW][GV_WAVES];  // EPI_ROPE: the passes' row sums (bias added)
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int K = a.K, nch = K / 8;
+  const int gph = EPI == EPI_ROPE ? a.hd / GV_WAVES : 1;  // passes per head (EPI_ROPE)
+  // weight row of this wave in pass r (-1: past the last row)
+  auto row_of = [&](int r, int& hh) -> int64_t {
+    const int gi = blockIdx.x * rpw + r;
+    hh = 0;
+    if constexpr (EPI == EPI_ROPE) {
+      hh = gi / gph;
+      const int j = gi % gph;
+      if (hh >= a.hq + 2 * a.hkv) return -1;
+      if (hh < a.hq + a.hkv) return (int64_t)hh * a.hd + (wv < 4 ? j * 4 + wv : a.hd / 2 + j * 4 + wv - 4);
+      return (int64_t)hh * a.hd + j * GV_WAVES + wv;
+    } else {
+      const int64_t row = (int64_t)gi * GV_WAVES + wv;
+      return row < a.N ? row : -1;
+    }
+  };
+  // the first GV_U weight chunks of pass 0 are queued before the prologue, so their latency
+  // overlaps the operand row's
+  int hh0;
+  const int64_t row0 = row_of(0, hh0);
+  const bool pre = row0 >= 0 && lane + 64 * (GV_U - 1) < nch;
+  u32x4_t avp[GV_U];
+  if (pre) {
+#pragma unroll
+    for (int u = 0; u < GV_U; ++u) avp[u] = ldg_nt(reinterpret_cast<const u32x4_t*>(a.w + row0 * K + (lane + 64 * u) * 8));
+  }
+  if constexpr (PRO == PRO_NONE) {
+    for (int c = threadIdx.x; c < nch; c += GV_WAVES * 64)
+      *reinterpret_cast<u32x4_t*>(xs + c * 8) = *reinterpret_cast<const u32x4_t*>(a.x + c * 8);
+    __syncthreads();
+  } else if constexpr (PRO == PRO_NORM) {
+    // ends with a barrier; work group 0 writes h + delta
+    add_rmsnorm_row<CPT>(a.x, a.delta, a.lnw, a.eps, K, rmsnorm_threads(K), blockIdx.x == 0 ? a.h_out : nullptr, xs,
+                         nred);
+  } else {
+    for (int c = threadIdx.x; c < nch; c += GV_WAVES * 64) {
+      const u32x4_t g = *reinterpret_cast<const u32x4_t*>(a.x + c * 8);
+      const u32x4_t u = *reinterpret_cast<const u32x4_t*>(a.x + a.inter + c * 8);
+      u32x4_t o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = pack_bf(silu_bf16(lo_bf(g[j])) * lo_bf(u[j]), silu_bf16(hi_bf(g[j])) * hi_bf(u[j]));
+      *reinterpret_cast<u32x4_t*>(xs + c * 8) = o;
+    }
+    __syncthreads();
+  }
+  for (int r = 0; r < rpw; ++r) {
+    int hh;
+    const int64_t row = row_of(r, hh);
+    if (row < 0) break;
+    const bf16_t* wr = a.w + row * K;
+    float acc = 0.f;
+    int c = lane;
+    for (; c + 64 * (GV_U - 1) < nch; c += 64 * GV_U) {
+      u32x4_t av[GV_U];
+      if (r == 0 && c == lane && pre) {
+#pragma unroll
+        for (int u = 0; u < GV_U; ++u) av[u] = avp[u];
+      } else {
+#pragma unroll
+        for (int u = 0; u < GV_U; ++u) av[u] = ldg_nt(reinterpret_cast<const u32x4_t*>(wr + (c + 64 * u) * 8));
+      }
+#pragma unroll
+      for (int u = 0; u < GV_U; ++u) {
+        const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(xs + (c + 64 * u) * 8);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc = fmaf(lo_bf(av[u][q]), lo_bf(bv[q]), acc);
+          acc = fmaf(hi_bf(av[u][q]), hi_bf(bv[q]), acc);
+        }
+      }
+    }
+    for (; c < nch; c += 64) {
+      const u32x4_t av = ldg_nt(reinterpret_cast<const u32x4_t*>(wr + c * 8));
+      const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(xs + c * 8);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc = fmaf(lo_bf(av[q]), lo_bf(bv[q]), acc);
+        acc = fmaf(hi_bf(av[q]), hi_bf(bv[q]), acc);
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+    if (a.bias) acc += bf2f(a.bias[row]);
+    if constexpr (EPI == EPI_ROPE) {
+      if (hh < a.hq + a.hkv) {
+        if (lane == 0) sums[r][wv] = acc;
+      } else if (lane == 0) {
+        const int64_t crow = a.rows[0];
+        if (crow >= 0 && crow < a.t_cap)
+          a.v_cache[((int64_t)(hh - a.hq - a.hkv) * a.t_cap + crow) * a.hd + (row - (int64_t)hh * a.hd)] = f2bf(acc);
+      }
+    } else {
+      if (lane == 0) a.y[row] = f2bf(acc);
+    }
+  }
+  if constexpr (EPI == EPI_ROPE) {
+    __syncthreads();
+    const int half_hd = a.hd / 2;
+    for (int t = threadIdx.x; t < rpw * 4; t += GV_WAVES * 64) {
+      const int r = t / 4, w = t % 4, gi = blockIdx.x * rpw + r, hh = gi / gph;
+      if (hh >= a.hq + a.hkv) continue;  // v heads (or past the last head): written already
+      const int d = (gi % gph) * 4 + w;
+      const float x1 = bf2f(f2bf(sums[r][w])), x2 = bf2f(f2bf(sums[r][w + 4]));
+      const float co = bf2f(a.cosb[d]), si = bf2f(a.sinb[d]);
+      const bf16_t o1 = f2bf(bf2f(f2bf(x1 * co)) + bf2f(f2bf(-x2 * si)));
+      const bf16_t o2 = f2bf(bf2f(f2bf(x2 * co)) + bf2f(f2bf(x1 * si)));
+      bf16_t* dst;
+      if (hh < a.hq) {
+        dst = a.q_out + (int64_t)hh * a.hd;
+      } else {
+        const int64_t crow = a.rows[0];
+        if (crow < 0 || crow >= a.t_cap) continue;
+        dst = a.k_cache + ((int64_t)(hh - a.hq) * a.t_cap + crow) * a.hd;
+      }
+      dst[d] = o1;
+      dst[d + half_hd] = o2;
+    }
+  }
+}
+
+// Passes per work group of gemv_kernel (8 rows per pass): one, up to 4 096 work groups, then as
+// few more as keep the launch under that (the prologue is repeated by every work group; 2 048 or
+// 768 work groups measured 3-16 % slower per step, 8 192 the same).
+static int gemv_rpw(int64_t groups) {
+  const int64_t most = 4096;
+  int rpw = 1;
+  while (rpw < GV_MAX_RPW && (groups + rpw - 1) / rpw > most) rpw *= 2;
+  return rpw;
+}
+
+template <int PRO, int EPI>
+static int launch_gemv(int cpt, const SkinnyArgs& a, int64_t groups, hipStream_t s) {
+  const int rpw = gemv_rpw(groups);
+  const dim3 grid((unsigned)((groups + rpw - 1) / rpw));
+  const size_t lds = (size_t)a.K * sizeof(bf16_t);
+  if constexpr (PRO == PRO_NORM) {
+    if (cpt <= 1) hipLaunchKernelGGL((gemv_kernel<PRO, 1, EPI>), grid, dim3(GV_WAVES * 64), lds, s, a, rpw);
+    else if (cpt <= 2) hipLaunchKernelGGL((gemv_kernel<PRO, 2, EPI>), grid, dim3(GV_WAVES * 64), lds, s, a, rpw);
+    else if (cpt <= 4) hipLaunchKernelGGL((gemv_kernel<PRO, 4, EPI>), grid, dim3(GV_WAVES * 64), lds, s, a, rpw);
+    else hipLaunchKernelGGL((gemv_kernel<PRO, 8, EPI>), grid, dim3(GV_WAVES * 64), lds, s, a, rpw);
+  } else {
+    hipLaunchKernelGGL((gemv_kernel<PRO, 1, EPI>), grid, dim3(GV_WAVES * 64), lds, s, a, rpw);
+  }
+  return check_launch("skinny gemv");
+}
+
 // Tile width: 16 features (twice the work groups, 64 contiguous weight bytes per row per step) for
 // one or two rows and fewer than 128 tiles of 32, measured faster there at one row: 11-17 % on a 7B
 // model's down projection (3 584 x 18 944, with and without the SiLU prologue) and 8 % on o
@@ -275,6 +446,9 @@ static int launch_skinny(int pro, int cpt, int tn, const SkinnyArgs& a, int ks, 
 // static arrays (partial tiles of the 32-feature tile, 32 KiB; norm scratch) and some headroom.
 constexpr size_t SK_STAGE_MAX = 160 * 1024 - sizeof(float) * (SK_WAVES * 16 * 64 + 32) - 256;
 
+// Dynamic LDS of gemv_kernel's operand row: 160 KiB less its static arrays and some headroom.
+constexpr size_t GV_STAGE_MAX = 160 * 1024 - sizeof(float) * (GV_MAX_RPW * GV_WAVES + 32) - 256;
+
 // K slices of the SiLU-gated projection: the plain rule, then more slices until this work group's
 // staged rows fit in LDS (0: no split fits).
 static int silu_ksplit(int tn, int64_t m, int64_t n, int64_t k) {
@@ -297,13 +471,13 @@ static int check_shape(const char* what, int64_t m, int64_t mmax, int64_t n, int
 }
 
 extern "C" size_t tread_skinny_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-  if (m <= 0 || m > 32 || n <= 0 || (n % 32) != 0 || k <= 0 || (k % (SK_WAVES * 16)) != 0) return 0;
+  if (m <= 1 || m > 32 || n <= 0 || (n % 32) != 0 || k <= 0 || (k % (SK_WAVES * 16)) != 0) return 0;
   const int ks = skinny_ksplit(skinny_tn(m, n, k), n, k);
   return ks > 1 ? (size_t)ks * m * n * sizeof(float) : 0;
 }
 
 extern "C" size_t tread_skinny_silu_workspace_bytes(int64_t m, int64_t n, int64_t inter) {
-  if (m <= 0 || m > 8 || n <= 0 || (n % 32) != 0 || inter <= 0 || (inter % (SK_WAVES * 16)) != 0) return 0;
+  if (m <= 1 || m > 8 || n <= 0 || (n % 32) != 0 || inter <= 0 || (inter % (SK_WAVES * 16)) != 0) return 0;
   const int ks = silu_ksplit(skinny_tn(m, n, inter), m, n, inter);
   return ks > 1 ? (size_t)ks * m * n * sizeof(float) : 0;
 }
@@ -316,8 +490,10 @@ extern "C" int tread_skinny_linear_bf16(const void* x, int64_t ldx, const void* 
   if (!x || !weight || !y) return fail(TREAD_EINVAL, "skinny_linear: null pointer");
   if (ldx < k || ldy < n || (ldx % 8) != 0) return fail(TREAD_EINVAL, "skinny_linear: bad leading dimensions");
   if ((((uintptr_t)x | (uintptr_t)weight) & 15) != 0) return fail(TREAD_EINVAL, "skinny_linear: x/weight not 16-byte aligned");
+  if (m == 1 && (size_t)k * sizeof(bf16_t) > GV_STAGE_MAX)
+    return fail(TREAD_EINVAL, "skinny_linear: a row of %lld does not fit in LDS", (long long)k);
   const int tn = skinny_tn(m, n, k);
-  int ks = skinny_ksplit(tn, n, k);
+  int ks = m == 1 ? 1 : skinny_ksplit(tn, n, k);
   if (ks > 1 && (!ws || ws_bytes < (size_t)ks * m * n * sizeof(float) || (((uintptr_t)ws) & 15) != 0)) ks = 1;
   SkinnyArgs a;
   memset(&a, 0, sizeof(a));
@@ -331,6 +507,7 @@ extern "C" int tread_skinny_linear_bf16(const void* x, int64_t ldx, const void* 
   a.M = (int)m;
   a.K = (int)k;
   a.N = (int)n;
+  if (m == 1) return launch_gemv<PRO_NONE, EPI_PLAIN>(1, a, n / GV_WAVES, (hipStream_t)stream);
   return launch_skinny(PRO_NONE, 1, tn, a, ks, 0, (hipStream_t)stream);
 }
 
@@ -361,6 +538,7 @@ extern "C" int tread_skinny_norm_linear_bf16(const void* h, const void* delta, c
   a.K = (int)k;
   a.N = (int)n;
   const int nthr = rmsnorm_threads((int)k), cpt = (int)((k / 8 + nthr - 1) / nthr);
+  if (m == 1) return launch_gemv<PRO_NORM, EPI_PLAIN>(cpt, a, n / GV_WAVES, (hipStream_t)stream);
   return launch_skinny(PRO_NORM, cpt, skinny_tn(m, n, k), a, 1, (size_t)m * k * sizeof(bf16_t), (hipStream_t)stream);
 }
 
@@ -408,6 +586,7 @@ extern "C" int tread_skinny_norm_qkv_rope_bf16(const void* h, const void* delta,
   a.hd = head_dim;
   const int tn = skinny_tn(m, n, hidden);  // the tile skinny_norm_linear picks: the same sums
   const int nthr = rmsnorm_threads((int)hidden), cpt = (int)((hidden / 8 + nthr - 1) / nthr);
+  if (m == 1) return launch_gemv<PRO_NORM, EPI_ROPE>(cpt, a, n / GV_WAVES, (hipStream_t)stream);
   launch_norm<EPI_ROPE>(cpt, tn, dim3((unsigned)(n / tn), 1), (size_t)m * hidden * sizeof(bf16_t), (hipStream_t)stream, a);
   return check_launch("skinny_norm_qkv_rope");
 }
@@ -419,6 +598,20 @@ extern "C" int tread_skinny_silu_linear_bf16(const void* gate_up, int64_t m, int
   if (!gate_up || !weight || !y) return fail(TREAD_EINVAL, "skinny_silu_linear: null pointer");
   if ((((uintptr_t)gate_up | (uintptr_t)weight) & 15) != 0)
     return fail(TREAD_EINVAL, "skinny_silu_linear: operands not 16-byte aligned");
+  if (m == 1) {
+    if ((size_t)inter * sizeof(bf16_t) > GV_STAGE_MAX)
+      return fail(TREAD_EINVAL, "skinny_silu_linear: a row of %lld does not fit in LDS", (long long)inter);
+    SkinnyArgs a;
+    memset(&a, 0, sizeof(a));
+    a.x = (const bf16_t*)gate_up;
+    a.inter = inter;
+    a.w = (const bf16_t*)weight;
+    a.y = (bf16_t*)y;
+    a.M = 1;
+    a.K = (int)inter;
+    a.N = (int)n;
+    return launch_gemv<PRO_SILU, EPI_PLAIN>(1, a, n / GV_WAVES, (hipStream_t)stream);
+  }
   const int tn = skinny_tn(m, n, inter);
   const int ks = silu_ksplit(tn, m, n, inter);
   if (ks == 0) return fail(TREAD_EINVAL, "skinny_silu_linear: %lld rows of %lld do not fit in LDS", (long long)m,
