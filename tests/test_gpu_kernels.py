@@ -205,7 +205,10 @@ def test_silu_mul_vs_torch():
                                              (17, 1024, 4096, False, 4096), (8, 3584, 18944, False, 18944),
                                              (1, 37888, 3584, False, 3584), (5, 32, 16384, True, 16384),
                                              (2, 2048, 2048, True, 2056), (2, 96, 16384, False, 16384),
-                                             (1, 3584, 18944, True, 18944)])
+                                             (1, 3584, 18944, True, 18944),
+                                             # one row over 16 388 groups of 8 features: 8 passes per
+                                             # work group, the last one partial; K of one chunk per lane
+                                             (1, 131104, 128, True, 128)])
 def test_skinny_linear_matches_fp32_reference(m, n, k, bias, ldx):
     """y = x W^T (+ b) of a few rows against the fp32 product of the same bf16 values: within one
     bf16 ulp of it plus the fp32 reordering error (1e-5 of the sum of |terms|, which matters only
@@ -254,29 +257,30 @@ def test_skinny_norm_linear_equals_norm_then_linear(m, H, n, with_delta, bias):
     assert torch.equal(y, _hip.skinny_linear(x, W, b))
 
 
-@pytest.mark.parametrize("m,H,hq,hkv,hd,bias", [
-    (1, 3584, 28, 4, 128, True),    # 7B decoding step: 32-feature tiles
-    (2, 3584, 28, 4, 128, True),
-    (1, 896, 14, 2, 64, True),      # 0.5B: 16-feature tiles (36 tiles of 32 would be too few)
-    (1, 8192, 64, 8, 128, False),   # 70B, no q|k|v bias
-    (3, 512, 8, 2, 64, False),
+@pytest.mark.parametrize("m,H,hq,hkv,hd,bias,oob", [
+    (1, 3584, 28, 4, 128, True, False),    # 7B decoding step (one row: one weight row per wave)
+    (2, 3584, 28, 4, 128, True, False),    # two rows: 32-feature MFMA tiles
+    (1, 896, 14, 2, 64, True, False),      # 0.5B
+    (1, 8192, 64, 8, 128, False, False),   # 70B, no q|k|v bias
+    (1, 512, 8, 2, 64, True, True),        # one row whose cache row is outside the cache, no delta
+    (3, 512, 8, 2, 64, False, True),
 ])
-def test_skinny_norm_qkv_rope_equals_norm_linear_then_rope_splice(m, H, hq, hkv, hd, bias):
-    """The fused q|k|v epilogue (paired feature tiles, RoPE, cache splice) gives the bits of
+def test_skinny_norm_qkv_rope_equals_norm_linear_then_rope_splice(m, H, hq, hkv, hd, bias, oob):
+    """The fused q|k|v epilogue (paired features, RoPE, cache splice) gives the bits of
     skinny_norm_linear followed by qkv_rope_splice: q, both cache layers (including the untouched
     rows and a row index outside the cache, which splices nothing) and h + delta."""
     g = torch.Generator().manual_seed(m * 31 + H + hq)
     n = (hq + 2 * hkv) * hd
     t_cap = 64
     h = torch.randn(m, H, generator=g).to(torch.bfloat16).to(DEV)
-    d = torch.randn(m, H, generator=g).to(torch.bfloat16).to(DEV)
+    d = None if (oob and m == 1) else torch.randn(m, H, generator=g).to(torch.bfloat16).to(DEV)
     lnw = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(DEV)
     W = (0.05 * torch.randn(n, H, generator=g)).to(torch.bfloat16).to(DEV)
     b = torch.randn(n, generator=g).to(torch.bfloat16).to(DEV) if bias else None
     pos = torch.tensor([5, 40, 63][:m], dtype=torch.int64, device=DEV)
     rows = pos.clone()
-    if m == 3:
-        rows[1] = t_cap + 7  # outside the cache: its k/v are not written
+    if oob:
+        rows[m // 2] = t_cap + 7  # outside the cache: its k/v are not written
     inv_freq = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).to(DEV)
     cos, sin = _hip.rope_table(pos, inv_freq, hd)
     K0 = torch.randn(1, hkv, t_cap, hd, generator=g).to(torch.bfloat16).to(DEV)
@@ -294,7 +298,7 @@ def test_skinny_norm_qkv_rope_equals_norm_linear_then_rope_splice(m, H, hq, hkv,
     assert torch.equal(hs, hs_ref)
     assert torch.equal(q, q_ref)
     assert torch.equal(K, K_ref) and torch.equal(V, V_ref)
-    assert not torch.equal(K, K0)  # the in-range rows were written
+    assert torch.equal(K, K0) == (oob and m == 1)  # in-range rows were written, none otherwise
 
 
 @pytest.mark.parametrize("m,inter,n", [(1, 18944, 3584), (8, 512, 256), (2, 4096, 64)])
