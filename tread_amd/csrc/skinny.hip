@@ -227,7 +227,10 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
 // pass's 8 rows are 4 (d, d + hd/2) pairs of a q or k head, rotated together once the passes are
 // done, or 8 rows of a v head, written to the cache directly.
 constexpr int GV_WAVES = 8;
-constexpr int GV_U = 4;  // 16-byte loads in flight per lane (2: 2 % slower per step; 8 spills at 64 VGPRs)
+// 16-byte loads in flight per lane: 7, one batch for a 3 584-wide operand row (7B decoding step:
+// 3.51 ms with 7, 3.54 with 4 plus the first batch queued before the prologue, 3.61 with 2; 8
+// leaves the 7-chunk rows to the one-chunk tail loop, 3.81)
+constexpr int GV_U = 7;
 constexpr int GV_MAX_RPW = 8;
 
 template <int PRO, int CPT, int EPI>
@@ -257,16 +260,6 @@ void gemv_kernel(const SkinnyArgs a, int rpw) {
       return row < a.N ? row : -1;
     }
   };
-  // the first GV_U weight chunks of pass 0 are queued before the prologue, so their latency
-  // overlaps the operand row's
-  int hh0;
-  const int64_t row0 = row_of(0, hh0);
-  const bool pre = row0 >= 0 && lane + 64 * (GV_U - 1) < nch;
-  u32x4_t avp[GV_U];
-  if (pre) {
-#pragma unroll
-    for (int u = 0; u < GV_U; ++u) avp[u] = ldg_nt(reinterpret_cast<const u32x4_t*>(a.w + row0 * K + (lane + 64 * u) * 8));
-  }
   if constexpr (PRO == PRO_NONE) {
     for (int c = threadIdx.x; c < nch; c += GV_WAVES * 64)
       *reinterpret_cast<u32x4_t*>(xs + c * 8) = *reinterpret_cast<const u32x4_t*>(a.x + c * 8);
@@ -295,13 +288,8 @@ void gemv_kernel(const SkinnyArgs a, int rpw) {
     int c = lane;
     for (; c + 64 * (GV_U - 1) < nch; c += 64 * GV_U) {
       u32x4_t av[GV_U];
-      if (r == 0 && c == lane && pre) {
 #pragma unroll
-        for (int u = 0; u < GV_U; ++u) av[u] = avp[u];
-      } else {
-#pragma unroll
-        for (int u = 0; u < GV_U; ++u) av[u] = ldg_nt(reinterpret_cast<const u32x4_t*>(wr + (c + 64 * u) * 8));
-      }
+      for (int u = 0; u < GV_U; ++u) av[u] = ldg_nt(reinterpret_cast<const u32x4_t*>(wr + (c + 64 * u) * 8));
 #pragma unroll
       for (int u = 0; u < GV_U; ++u) {
         const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(xs + (c + 64 * u) * 8);
