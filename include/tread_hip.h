@@ -23,7 +23,7 @@ typedef void* tread_event_t;  /* hipEvent_t */
 
 /* Thread-local text of the last error (empty string if none). */
 const char* tread_last_error(void);
-/* ABI version of this header (9); bumps on any signature change. */
+/* ABI version of this header (10); bumps on any signature change. */
 int tread_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------
@@ -176,6 +176,18 @@ int tread_skinny_norm_qkv_rope_bf16(const void* h, const void* delta, const void
                                     int64_t hidden, const void* wqkv, const void* bqkv, int hq, int hkv, int head_dim,
                                     const void* cos, const void* sin, const int64_t* rows, void* q_out, void* k_cache,
                                     void* v_cache, int64_t t_cap, void* h_out, tread_stream_t stream);
+
+/* skinny_norm_linear of an MLP's gate|up projection with silu_mul fused behind it: for m <= 8 rows,
+ * [g | u] = linear(RMSNorm(h + delta), wgu) (wgu: [2 inter, hidden], gate rows then up rows;
+ * inter a multiple of 16) and y [m, inter] = bf16(bf16(silu(g)) * u), h_out = h + delta (may be
+ * NULL). Bits equal to tread_skinny_norm_linear_bf16 followed by tread_silu_mul_bf16, in one
+ * launch, without the [m, 2 inter] intermediate. Replaces post_attention_layernorm + gate/up
+ * projections + act_fn(gate) * up of a decoding step (transformers Qwen2MLP under
+ * tread/server.py:207).
+ */
+int tread_skinny_norm_swiglu_bf16(const void* h, const void* delta, const void* ln_weight, float eps, int64_t m,
+                                  int64_t hidden, const void* wgu, int64_t inter, void* y, void* h_out,
+                                  tread_stream_t stream);
 
 /* y[m, n] = linear(bf16(bf16(silu(g)) * u)) for gate_up [m, 2 inter] = [g | u], m <= 8 (silu_mul's
  * bits fused into the down projection of a decoding step, transformers Qwen2MLP). ws: at least

@@ -301,6 +301,23 @@ def test_skinny_norm_qkv_rope_equals_norm_linear_then_rope_splice(m, H, hq, hkv,
     assert torch.equal(K, K0) == (oob and m == 1)  # in-range rows were written, none otherwise
 
 
+@pytest.mark.parametrize("m,H,inter,with_delta", [(1, 3584, 18944, True), (2, 3584, 18944, True),
+                                                 (1, 896, 4864, False), (1, 8192, 28672, True),
+                                                 (3, 512, 1024, True), (8, 256, 272, False)])
+def test_skinny_norm_swiglu_equals_norm_linear_then_silu_mul(m, H, inter, with_delta):
+    """The fused gate|up epilogue (gate and up rows paired in one tile or pass) gives the bits of
+    skinny_norm_linear followed by silu_mul, and h + delta."""
+    g = torch.Generator().manual_seed(m * 13 + H + inter)
+    h = torch.randn(m, H, generator=g).to(torch.bfloat16).to(DEV)
+    d = torch.randn(m, H, generator=g).to(torch.bfloat16).to(DEV) if with_delta else None
+    lnw = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(DEV)
+    W = (0.05 * torch.randn(2 * inter, H, generator=g)).to(torch.bfloat16).to(DEV)
+    act, hs = _hip.skinny_norm_swiglu(h, d, lnw, 1e-6, W)
+    gu, hs_ref = _hip.skinny_norm_linear(h, d, lnw, 1e-6, W)
+    assert torch.equal(hs, hs_ref)
+    assert torch.equal(act, _hip.silu_mul(gu))
+
+
 @pytest.mark.parametrize("m,inter,n", [(1, 18944, 3584), (8, 512, 256), (2, 4096, 64)])
 def test_skinny_silu_linear_equals_silu_mul_then_linear(m, inter, n):
     g = torch.Generator().manual_seed(m + inter)

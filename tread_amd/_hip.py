@@ -10,7 +10,7 @@ from pathlib import Path
 import torch  # loads torch's HIP runtime first, so the library below binds to the same one
 
 LIB_PATH = Path(__file__).resolve().with_name("libtread_hip.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 c_i64, c_int, c_void, c_float, c_size = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
 P_I64 = ctypes.POINTER(ctypes.c_int64)
@@ -49,6 +49,8 @@ _SIGS = {
     "tread_skinny_norm_qkv_rope_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_i64, c_void, c_void, c_int,
                                                 c_int, c_int, c_void, c_void, c_void, c_void, c_void, c_void, c_i64,
                                                 c_void, c_void]),
+    "tread_skinny_norm_swiglu_bf16": (c_int, [c_void, c_void, c_void, c_float, c_i64, c_i64, c_void, c_i64, c_void,
+                                              c_void, c_void]),
     "tread_skinny_silu_workspace_bytes": (c_size, [c_i64, c_i64, c_i64]),
     "tread_skinny_silu_linear_bf16": (c_int, [c_void, c_i64, c_i64, c_void, c_i64, c_void, c_void, c_size, c_void]),
     "tread_copy_async": (c_int, [c_void, c_void, c_size, c_void, c_void]),
@@ -304,6 +306,28 @@ def skinny_norm_qkv_rope(h, delta, ln_w, eps, wqkv, bqkv, hq, hkv, hd, cos, sin,
         _ptr(h), _ptr(delta), _ptr(ln_w), float(eps), m, k, _ptr(wqkv), _ptr(bqkv), hq, hkv, hd, _ptr(cos),
         _ptr(sin), _ptr(rows), _ptr(q_out), _ptr(k_cache), _ptr(v_cache), t_cap, _ptr(h_out), _stream()))
     return h_out if h_out is not None else h
+
+
+def skinny_norm_swiglu(h, delta, ln_w, eps, wgu):
+    """(bf16(silu(g)) * u, h + delta) for a few rows h [m, k], [g | u] = linear(RMSNorm(h + delta),
+    wgu) (wgu [2 inter, k]): the MLP's norm, gate|up and SiLU gating in one launch, the same bits
+    as skinny_norm_linear followed by silu_mul. delta may be None (then h itself comes back)."""
+    _need(h, "h")
+    _need(wgu, "wgu")
+    _need(ln_w, "ln_w")
+    if delta is not None:
+        _need(delta, "delta")
+    m, k = h.shape
+    n = wgu.shape[0]
+    inter = n // 2
+    if (wgu.shape[1] != k or n % 2 or inter % 16 or not norm_fused_ok(m, n, k)
+            or (delta is not None and delta.shape != h.shape)):
+        raise ValueError(f"skinny_norm_swiglu: unsupported shape h {tuple(h.shape)} wgu {tuple(wgu.shape)}")
+    y = torch.empty(m, inter, dtype=h.dtype, device=h.device)
+    h_out = torch.empty_like(h) if delta is not None else None
+    _check("tread_skinny_norm_swiglu_bf16", lib().tread_skinny_norm_swiglu_bf16(
+        _ptr(h), _ptr(delta), _ptr(ln_w), float(eps), m, k, _ptr(wgu), inter, _ptr(y), _ptr(h_out), _stream()))
+    return y, (h_out if h_out is not None else h)
 
 
 def skinny_silu_linear(gate_up, weight):

@@ -34,7 +34,7 @@ int check_launch(const char* what) {
 
 extern "C" const char* tread_last_error(void) { return tread::g_err; }
 
-extern "C" int tread_abi_version(void) { return 9; }
+extern "C" int tread_abi_version(void) { return 10; }
 
 extern "C" int tread_copy_layers_async(void* const* dst, const void* const* src, const size_t* bytes, int per_layer,
                                        int n_layers, tread_stream_t stream, const tread_event_t* layer_done) {

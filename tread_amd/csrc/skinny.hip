@@ -37,6 +37,8 @@ struct SkinnyArgs {
   int64_t ldy;
   float* part;
   int M, K, N;
+  // EPI_SWIGLU: gate|up of an MLP (N = 2 inter, the weight's rows [gate; up]): y [M, inter] =
+  // bf16(bf16(silu(g)) * u) with g, u rounded to bf16 first (silu_mul's bits)
   // EPI_ROPE: q|k|v of a decoder layer (N = (hq + 2 hkv) hd): q and k rotated (cos / sin [M, hd / 2])
   // into q_out [M, hq, hd] and k_cache, v into v_cache, row rows[m] of each [hkv, t_cap, hd] cache
   const bf16_t* cosb;
@@ -49,7 +51,7 @@ struct SkinnyArgs {
   int hq, hkv, hd;
 };
 
-enum { EPI_PLAIN = 0, EPI_ROPE = 1 };
+enum { EPI_PLAIN = 0, EPI_ROPE = 1, EPI_SWIGLU = 2 };
 
 // blockIdx.y = q selects the K slice [q K / ks, (q + 1) K / ks); with ks > 1 the slice's fp32 sums
 // go to part[q][m][n] and skinny_reduce_kernel finishes them.
@@ -83,6 +85,9 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_gemm_kernel(const Skinny
     const int tph = a.hd / TN, hh = blockIdx.x / tph, p = blockIdx.x % tph;
     if (hh < a.hq + a.hkv)
       wrow = (int64_t)hh * a.hd + (rt < TN / 2 ? p * (TN / 2) + rt : a.hd / 2 + p * (TN / 2) + rt - TN / 2);
+  } else if constexpr (EPI == EPI_SWIGLU) {  // tile p: gate rows then the matching up rows
+    const int64_t j0 = (int64_t)blockIdx.x * (TN / 2);
+    wrow = rt < TN / 2 ? j0 + rt : a.inter + j0 + rt - TN / 2;
   }
   const bf16_t* wp = a.w + wrow * (int64_t)K + kb;
   const bool xon = rt < M;
@@ -192,6 +197,19 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_gemm_kernel(const Skinny
     }
     return;
   }
+  if constexpr (EPI == EPI_SWIGLU) {
+    for (int t = threadIdx.x; t < (TN / 2) * M; t += SK_WAVES * 64) {
+      const int m = t / (TN / 2), pr = t % (TN / 2);
+      const int64_t j = (int64_t)blockIdx.x * (TN / 2) + pr;
+      float g = tile_sum(m, pr), u = tile_sum(m, pr + TN / 2);
+      if (a.bias) {
+        g += bf2f(a.bias[j]);
+        u += bf2f(a.bias[a.inter + j]);
+      }
+      a.y[(int64_t)m * a.inter + j] = f2bf(silu_bf16(bf2f(f2bf(g))) * bf2f(f2bf(u)));
+    }
+    return;
+  }
   for (int t = threadIdx.x; t < TN * M; t += SK_WAVES * 64) {
     const int m = t / TN, row = t % TN;
     float v = tile_sum(m, row);
@@ -241,7 +259,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) __attribute__((amdgpu_waves_per_eu(C
 void gemv_kernel(const SkinnyArgs a, int rpw) {
   extern __shared__ __align__(16) bf16_t xs[];  // the operand row [K]
   __shared__ float nred[32];
-  __shared__ float sums[GV_MAX_RPW][GV_WAVES];  // EPI_ROPE: the passes' row sums (bias added)
+  __shared__ float sums[GV_MAX_RPW][GV_WAVES];  // EPI_ROPE / EPI_SWIGLU: the passes' row sums (bias added)
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int K = a.K, nch = K / 8;
   const int gph = EPI == EPI_ROPE ? a.hd / GV_WAVES : 1;  // passes per head (EPI_ROPE)
@@ -255,6 +273,10 @@ void gemv_kernel(const SkinnyArgs a, int rpw) {
       if (hh >= a.hq + 2 * a.hkv) return -1;
       if (hh < a.hq + a.hkv) return (int64_t)hh * a.hd + (wv < 4 ? j * 4 + wv : a.hd / 2 + j * 4 + wv - 4);
       return (int64_t)hh * a.hd + j * GV_WAVES + wv;
+    } else if constexpr (EPI == EPI_SWIGLU) {  // pass gi: gate rows 4 gi .. 4 gi + 3, then their up rows
+      const int64_t j = (int64_t)gi * 4;
+      if (j >= a.inter) return -1;
+      return wv < 4 ? j + wv : a.inter + j + wv - 4;
     } else {
       const int64_t row = (int64_t)gi * GV_WAVES + wv;
       return row < a.N ? row : -1;
@@ -320,8 +342,19 @@ void gemv_kernel(const SkinnyArgs a, int rpw) {
         if (crow >= 0 && crow < a.t_cap)
           a.v_cache[((int64_t)(hh - a.hq - a.hkv) * a.t_cap + crow) * a.hd + (row - (int64_t)hh * a.hd)] = f2bf(acc);
       }
+    } else if constexpr (EPI == EPI_SWIGLU) {
+      if (lane == 0) sums[r][wv] = acc;
     } else {
       if (lane == 0) a.y[row] = f2bf(acc);
+    }
+  }
+  if constexpr (EPI == EPI_SWIGLU) {
+    __syncthreads();
+    for (int t = threadIdx.x; t < rpw * 4; t += GV_WAVES * 64) {
+      const int r = t / 4, w = t % 4;
+      const int64_t j = (int64_t)(blockIdx.x * rpw + r) * 4 + w;
+      if (j >= a.inter) continue;
+      a.y[j] = f2bf(silu_bf16(bf2f(f2bf(sums[r][w]))) * bf2f(f2bf(sums[r][w + 4])));
     }
   }
   if constexpr (EPI == EPI_ROPE) {
@@ -577,6 +610,42 @@ extern "C" int tread_skinny_norm_qkv_rope_bf16(const void* h, const void* delta,
   if (m == 1) return launch_gemv<PRO_NORM, EPI_ROPE>(cpt, a, n / GV_WAVES, (hipStream_t)stream);
   launch_norm<EPI_ROPE>(cpt, tn, dim3((unsigned)(n / tn), 1), (size_t)m * hidden * sizeof(bf16_t), (hipStream_t)stream, a);
   return check_launch("skinny_norm_qkv_rope");
+}
+
+extern "C" int tread_skinny_norm_swiglu_bf16(const void* h, const void* delta, const void* ln_weight, float eps,
+                                             int64_t m, int64_t hidden, const void* wgu, int64_t inter, void* y,
+                                             void* h_out, tread_stream_t stream) {
+  if (m == 0) return 0;
+  if (inter <= 0 || (inter % 16) != 0)
+    return fail(TREAD_EINVAL, "skinny_norm_swiglu: inter %lld must be a positive multiple of 16", (long long)inter);
+  const int64_t n = 2 * inter;
+  if (int rc = check_shape("skinny_norm_swiglu", m, 8, n, hidden)) return rc;
+  if (hidden > 16384) return fail(TREAD_EINVAL, "skinny_norm_swiglu: hidden %lld above 16384", (long long)hidden);
+  if ((size_t)m * hidden * sizeof(bf16_t) > SK_STAGE_MAX)
+    return fail(TREAD_EINVAL, "skinny_norm_swiglu: %lld rows of %lld do not fit in LDS", (long long)m,
+                (long long)hidden);
+  if (!h || !ln_weight || !wgu || !y) return fail(TREAD_EINVAL, "skinny_norm_swiglu: null pointer");
+  if ((((uintptr_t)h | (uintptr_t)delta | (uintptr_t)ln_weight | (uintptr_t)wgu | (uintptr_t)h_out) & 15) != 0)
+    return fail(TREAD_EINVAL, "skinny_norm_swiglu: operands not 16-byte aligned");
+  SkinnyArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = (const bf16_t*)h;
+  a.ldx = hidden;
+  a.delta = (const bf16_t*)delta;
+  a.lnw = (const bf16_t*)ln_weight;
+  a.eps = eps;
+  a.h_out = (bf16_t*)h_out;
+  a.w = (const bf16_t*)wgu;
+  a.inter = inter;
+  a.y = (bf16_t*)y;
+  a.M = (int)m;
+  a.K = (int)hidden;
+  a.N = (int)n;
+  const int tn = skinny_tn(m, n, hidden);  // the tile skinny_norm_linear picks: the same sums
+  const int nthr = rmsnorm_threads((int)hidden), cpt = (int)((hidden / 8 + nthr - 1) / nthr);
+  if (m == 1) return launch_gemv<PRO_NORM, EPI_SWIGLU>(cpt, a, n / GV_WAVES, (hipStream_t)stream);
+  launch_norm<EPI_SWIGLU>(cpt, tn, dim3((unsigned)(n / tn), 1), (size_t)m * hidden * sizeof(bf16_t), (hipStream_t)stream, a);
+  return check_launch("skinny_norm_swiglu");
 }
 
 extern "C" int tread_skinny_silu_linear_bf16(const void* gate_up, int64_t m, int64_t inter, const void* weight,

@@ -133,6 +133,10 @@ def _layer_few_rows(P, l, lw, h, delta, R, K, V):
         _hip.qkv_rope_splice(qkv, R.cos, R.sin, R.rows, hq, hkv, hd, K[l], V[l], q_out=q)
     o = _hip.subset_attn(q, K[l], V[l], R.kend, hq, hkv, hd, P.scale, kseg=R.kseg, n_shared=R.n_shared)
     a = _hip.skinny_linear(o, lw.wo)
+    if m <= NORM_FUSED_ROWS and _hip.norm_fused_ok(m, lw.wgu.shape[0], lw.wgu.shape[1]):
+        # norm, gate|up and SiLU gating in one launch (silu_mul's bits), then a plain down projection
+        act, h = _hip.skinny_norm_swiglu(h, a, lw.ln2, P.eps, lw.wgu)
+        return h, _hip.skinny_linear(act, lw.wd)
     gu, h = _norm_linear(P, h, a, lw.ln2, lw.wgu)
     return h, _silu_linear(gu, lw.wd)
 
