@@ -658,8 +658,8 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
 // same MFMA layouts on one 32-key block, and keeps its own running max and sums. No wave waits for
 // another inside the loop: a wave queues its next K tile as soon as its score MFMAs have read this
 // one, and its next V tile after its PV MFMAs, so its loads overlap its own arithmetic and the
-// other wave of its SIMD; its first K tile is queued before the rows' key ends are even read. At
-// the end the 8 waves' (max, sum, O) meet in LDS; one partial per row
+// other wave of its SIMD; its first K and V tiles go out together once the rows' key ends are in.
+// At the end the 8 waves' (max, sum, O) meet in LDS; one partial per row
 // goes to the split-K workspace for the combine kernels, or, with a single slice, the normalised
 // output is written directly.
 constexpr int DEC_WAVES = 8;
@@ -701,43 +701,50 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_attn_kernel(const AttnArgs
       lds_load16(base + grow * HD + (ch ^ sw) * 8, buf + x * 64 * 8);
     }
   };
-  // The K rows of the wave's first tile are queued before the rows' key ends are read: bounded by
-  // the slice and the cache only (finite data; keys past a row's end are masked from the scores, so
-  // they never reach P V). V rows are only read up to the last visible key.
-  {
-    const int k0 = k_lo + wv * DEC_BK, k1 = min(min(k0 + DEC_BK, k_lo + a.split_len), (int)a.t_cap);
-    if (k0 < k1) issue(k0, k1, kbase, kbuf, false);
-  }
+  // The rows' key ends and Q are loaded before any tile: the compiler waits for all outstanding
+  // vector memory (vmcnt(0)) before using a plain load's value while global -> LDS loads are in
+  // flight, so these go first, and the wave's first K and V tiles follow together. A lane past the
+  // launch's rows reads row 0 (unconditional loads: one under a branch is waited for at its end);
+  // its column's scores and output are never used.
   const int64_t R = a.n * a.G;
   const bool valid = c < R;  // this lane's query column: row c = (token c / G, head head * G + c % G)
   const int64_t qi = valid ? c / a.G : 0;
   const int qh = head * a.G + (int)(valid ? c % a.G : 0);
   const int n_shared = a.kseg ? (int)min<int64_t>(a.n_shared, a.t_cap) : 0;
-  int my_end = -1, my_seg = 0;
-  if (valid) {
-    my_end = (int)min<int64_t>(max<int64_t>(a.kend[qi], -1), a.t_cap - 1);
-    if (a.kseg) my_seg = (int)min<int64_t>(max<int64_t>(a.kseg[qi], 0), a.t_cap);
+  const int64_t end_raw = a.kend[qi];
+  const int64_t seg_raw = (a.kseg ? a.kseg : a.kend)[qi];
+  u32x4_t qraw[KS];
+  {
+    const bf16_t* qp = a.q + (qi * a.hq + qh) * HD + half * 8;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qraw[s] = *reinterpret_cast<const u32x4_t*>(qp + s * 16);
   }
+  const int64_t tcap1 = a.t_cap - 1;
+  const int my_end = !valid ? -1 : (int)(end_raw < -1 ? -1 : end_raw > tcap1 ? tcap1 : end_raw);
+  const int my_seg = !(valid && a.kseg) ? 0 : (int)(seg_raw < 0 ? 0 : seg_raw > a.t_cap ? a.t_cap : seg_raw);
   // every wave holds the same rows, so wave reductions give the work group's key bounds
   const int kmax = wave_max(my_end);
   const int kmin = wave_min(valid ? my_end : 0x7fffffff);
   const int segmax = wave_max(valid && a.kseg ? my_seg : 0);
   const int k_hi = min(k_lo + a.split_len, kmax + 1);
   const int ntiles = k_hi > k_lo ? (k_hi - k_lo + DEC_BK - 1) / DEC_BK : 0;
-
   // Q^T fragments (B operand), pre-multiplied by scale * log2(e) and rounded to bf16, as in
-  // subset_attn_kernel
+  // subset_attn_kernel (before the tile loads go out, for the reason above)
   bf16x8_t qf[KS];
-  {
-    const bf16_t* qp = a.q + (qi * a.hq + qh) * HD + half * 8;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      u32x4_t t = {0, 0, 0, 0};
-      if (valid) t = *reinterpret_cast<const u32x4_t*>(qp + s * 16);
+  for (int s = 0; s < KS; ++s) {
+    u32x4_t t = qraw[s];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) t[w] = pack_bf(lo_bf(t[w]) * a.scale_log2, hi_bf(t[w]) * a.scale_log2);
-      qf[s] = __builtin_bit_cast(bf16x8_t, t);
-    }
+    for (int w = 0; w < 4; ++w) t[w] = pack_bf(lo_bf(t[w]) * a.scale_log2, hi_bf(t[w]) * a.scale_log2);
+    qf[s] = __builtin_bit_cast(bf16x8_t, t);
+    asm volatile("" : "+v"(qf[s]));  // computed here, not next to its first use
+  }
+  // K rows only up to the last visible key as well: keys past a row's end are masked from the
+  // scores, and V rows past the work group's last visible key are never read
+  if (wv < ntiles) {
+    const int k0 = k_lo + wv * DEC_BK, k1 = min(k0 + DEC_BK, k_hi);
+    issue(k0, k1, kbase, kbuf, false);
+    issue(k0, k1, vbase, vbuf, true);
   }
 
   auto tile_keys = [&](int j, int& k0, int& k1) {
@@ -779,13 +786,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_attn_kernel(const AttnArgs
   float m_run = -INFINITY;  // log2-scaled running max of this lane's row (-inf: nothing visible yet)
   float lsum[4] = {0.f, 0.f, 0.f, 0.f};
 
-  int j = wv;
-  if (j < ntiles) {
-    int k0, k1;
-    tile_keys(j, k0, k1);
-    issue(k0, k1, vbase, vbuf, true);
-  }
-  for (; j < ntiles; j += DEC_WAVES) {
+  for (int j = wv; j < ntiles; j += DEC_WAVES) {
     const int jn = j + DEC_WAVES;
     const bool more = jn < ntiles;
     vm_wait<LPK>();  // this tile's K landed (its V may still fly)
@@ -877,28 +878,32 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_attn_kernel(const AttnArgs
       issue(n0, n1, vbase, vbuf, true);
     }
   }
-  vm_wait<0>();  // a first K tile queued for a wave without tiles lands before its LDS is reused
 
   // ---- merge the 8 waves' partials of each row
   const float l_row = xhalf_sum((lsum[0] + lsum[1]) + (lsum[2] + lsum[3]));
   __syncthreads();  // every wave is done with its tile buffers
-  float* const mo = reinterpret_cast<float*>(smem);  // [wave][row][HD]
+  // [wave][row][HD + 4]: the 16-byte pad per row puts the 32 rows a store instruction writes in
+  // different banks (with a stride of HD floats every lane of a store hit the same banks, and the
+  // 8 waves' writes took 3.5 us)
+  constexpr int MO_LD = HD + 4;
+  float* const mo = reinterpret_cast<float*>(smem);
+  if (valid) {  // only the launch's rows are merged
 #pragma unroll
-  for (int d = 0; d < DB; ++d)
+    for (int d = 0; d < DB; ++d)
 #pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const f32x4_t o = {oacc[d][g4 * 4 + 0], oacc[d][g4 * 4 + 1], oacc[d][g4 * 4 + 2], oacc[d][g4 * 4 + 3]};
-      *reinterpret_cast<f32x4_t*>(mo + (wv * DEC_ROWS + c) * HD + d * 32 + g4 * 8 + half * 4) = o;
-    }
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const f32x4_t o = {oacc[d][g4 * 4 + 0], oacc[d][g4 * 4 + 1], oacc[d][g4 * 4 + 2], oacc[d][g4 * 4 + 3]};
+        *reinterpret_cast<f32x4_t*>(mo + (wv * DEC_ROWS + c) * MO_LD + d * 32 + g4 * 8 + half * 4) = o;
+      }
+  }
   if (half == 0) {
     mrg_m[wv][c] = m_run;
     mrg_l[wv][c] = l_row;
   }
   __syncthreads();
   constexpr int DQ = HD / 4;
-  for (int it = threadIdx.x; it < DEC_ROWS * DQ; it += DEC_THREADS) {
+  for (int it = threadIdx.x; it < (int)R * DQ; it += DEC_THREADS) {
     const int rr = it / DQ, dq = it % DQ;
-    if (rr >= R) continue;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < DEC_WAVES; ++w)
@@ -911,7 +916,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_attn_kernel(const AttnArgs
       if (l > 0.f) {
         const float wgt = __builtin_amdgcn_exp2f(mrg_m[w][rr] - M);
         L += wgt * l;
-        acc += wgt * *reinterpret_cast<const f32x4_t*>(mo + (w * DEC_ROWS + rr) * HD + dq * 4);
+        acc += wgt * *reinterpret_cast<const f32x4_t*>(mo + (w * DEC_ROWS + rr) * MO_LD + dq * 4);
       }
     }
     if (a.nsplit > 1) {
@@ -951,9 +956,25 @@ __global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(const AttnArg
   const int64_t stride = (int64_t)a.hkv * a.tiles * a.prow;
   const int64_t p0 = ((int64_t)head * a.tiles + tile) * a.prow + in_tile;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int dq = t % DQ, sg = t / DQ;  // this thread's 4 output elements and split group
+  // The (max, sum) of slice t and the split group's first UNR partial rows are all issued before any
+  // of them is used: one round of memory latency when nsplit <= UNR * SG (a decoding step's 64
+  // slices), where the maxima, then the weights, then the rows took three.
+  constexpr int UNR = 8;
+  f32x4_t o[UNR];
+  auto load_rows = [&](int s0) {
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int s = s0 + u * SG;
+      if (s < a.nsplit) o[u] = *reinterpret_cast<const f32x4_t*>(a.ws_o + (p0 + s * stride) * HD + dq * 4);
+    }
+  };
+  float2 ml0 = {0.f, 0.f};
+  if (t < a.nsplit) ml0 = *reinterpret_cast<const float2*>(a.ws_ml + (p0 + t * stride) * 2);
+  load_rows(sg);
   // global max of the split maxima
-  float m = -INFINITY;
-  for (int s = t; s < a.nsplit; s += CMB_THREADS)
+  float m = ml0.y > 0.f ? ml0.x : -INFINITY;
+  for (int s = t + CMB_THREADS; s < a.nsplit; s += CMB_THREADS)
     if (a.ws_ml[(p0 + s * stride) * 2 + 1] > 0.f) m = fmaxf(m, a.ws_ml[(p0 + s * stride) * 2]);
   m = wave_max_f(m);
   if (lane == 0) red[wv] = m;
@@ -964,7 +985,12 @@ __global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(const AttnArg
   __syncthreads();
   // weights and the weighted sum of the split sums
   float lw = 0.f;
-  for (int s = t; s < a.nsplit; s += CMB_THREADS) {
+  if (t < a.nsplit) {
+    const float wgt = ml0.y > 0.f ? __builtin_amdgcn_exp2f(ml0.x - M) : 0.f;
+    sm_w[t] = wgt;
+    lw += wgt * ml0.y;
+  }
+  for (int s = t + CMB_THREADS; s < a.nsplit; s += CMB_THREADS) {
     const int64_t p = p0 + s * stride;
     const float l = a.ws_ml[p * 2 + 1];
     const float wgt = l > 0.f ? __builtin_amdgcn_exp2f(a.ws_ml[p * 2] - M) : 0.f;
@@ -977,23 +1003,18 @@ __global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(const AttnArg
   float L = 0.f;
 #pragma unroll
   for (int q = 0; q < CMB_THREADS / 64; ++q) L += red[q];
-  // this thread's 4 elements over its split group
-  const int dq = t % DQ, sg = t / DQ;
-  // the group's slices four at a time: their loads go out together, the sum keeps slice order
+  // the group's slices in order, UNR at a time (empty slices have weight 0 and are skipped)
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  constexpr int UNR = 4;
-  for (int s0 = sg; s0 < a.nsplit; s0 += UNR * SG) {
-    f32x4_t o[UNR];
-    float wg[UNR];
+  for (int s0 = sg;;) {
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
       const int s = s0 + u * SG;
-      wg[u] = s < a.nsplit ? sm_w[s] : 0.f;
-      if (wg[u] != 0.f) o[u] = *reinterpret_cast<const f32x4_t*>(a.ws_o + (p0 + s * stride) * HD + dq * 4);
+      const float wg = s < a.nsplit ? sm_w[s] : 0.f;
+      if (wg != 0.f) acc += wg * o[u];
     }
-#pragma unroll
-    for (int u = 0; u < UNR; ++u)
-      if (wg[u] != 0.f) acc += wg[u] * o[u];
+    s0 += UNR * SG;
+    if (s0 >= a.nsplit) break;
+    load_rows(s0);
   }
   part[sg][dq] = acc;
   __syncthreads();
@@ -1213,7 +1234,8 @@ static int launch_combine(const AttnArgs& a, int head_dim, hipStream_t s) {
 static int decode_attn_launch(AttnArgs& a, const SplitPlan& sp, int head_dim, hipStream_t s) {
   a.prow = DEC_ROWS;
   const dim3 grid((unsigned)sp.nsplit, (unsigned)a.hkv);
-  const size_t smem = (size_t)DEC_WAVES * DEC_ROWS * head_dim * sizeof(float);  // = 8 waves' K and V tiles
+  // the 8 waves' padded fp32 O rows of the merge (slightly more than their K and V tiles)
+  const size_t smem = (size_t)DEC_WAVES * DEC_ROWS * (head_dim + 4) * sizeof(float);
   if (head_dim == 128)
     hipLaunchKernelGGL(decode_attn_kernel<128>, grid, dim3(DEC_THREADS), smem, s, a);
   else
