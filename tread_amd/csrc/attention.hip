@@ -177,6 +177,12 @@ __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Work-group barrier of the tile pipelines, after each wave has waited (vm_wait) for its own
+// global->LDS loads of the tiles the barrier publishes. __syncthreads() would also wait for every
+// outstanding vector memory operation (vmcnt(0)), i.e. for the tiles still being prefetched,
+// taking the pipeline's load lead away at every barrier.
+__device__ __forceinline__ void tile_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // max over lanes l and l ^ 32 (the two key halves of one query column)
 __device__ __forceinline__ float xhalf_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -534,7 +540,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
         if (ntiles > 1) vm_wait<LPT>();
         else vm_wait<0>();
       }
-      __syncthreads();
+      tile_barrier();
       int bj = 0;
       for (int j = 0; j + 1 < ntiles; ++j) {
         if constexpr (ATT_NBUF >= 4) {
@@ -543,7 +549,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
         } else {
           vm_wait<0>();
         }
-        __syncthreads();
+        tile_barrier();
         const int bn = bj == ATT_NBUF - 1 ? 0 : bj + 1, bprev = bj == 0 ? ATT_NBUF - 1 : bj - 1;
         const int tl = j + ATT_NBUF - 1;
         if (tl < ntiles) issue_tile(tl, bprev);
@@ -565,7 +571,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       if (ntiles > 1) vm_wait<LPT>();
       else vm_wait<0>();
     }
-    __syncthreads();
+    tile_barrier();
     const bool late = wv >= ATT_WAVES / 2;
     f32x16_t sc[2];
     bf16x8_t pb[4];
@@ -584,7 +590,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       } else {
         vm_wait<0>();
       }
-      __syncthreads();
+      tile_barrier();
       const int bn = bj == ATT_NBUF - 1 ? 0 : bj + 1, bprev = bj == 0 ? ATT_NBUF - 1 : bj - 1;
       const int tl = j + ATT_NBUF - 1;
       if (tl < ntiles) issue_tile(tl, bprev);
