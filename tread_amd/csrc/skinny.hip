@@ -247,7 +247,8 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
 constexpr int GV_WAVES = 8;
 // 16-byte loads in flight per lane: 7, one batch for a 3 584-wide operand row (7B decoding step:
 // 3.51 ms with 7, 3.54 with 4 plus the first batch queued before the prologue, 3.61 with 2; 8
-// leaves the 7-chunk rows to the one-chunk tail loop, 3.81)
+// leaves the 7-chunk rows to the one-chunk tail loop, 3.81; later, 7 with the first batch queued
+// before the prologue: 3.33 against 3.30)
 constexpr int GV_U = 7;
 constexpr int GV_MAX_RPW = 8;
 
