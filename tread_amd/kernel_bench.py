@@ -1,7 +1,7 @@
 """Kernel micro-benchmarks on synthetic inputs of the reuse workloads' shapes.
 
     python -m tread_amd.kernel_bench assemble  [--workload qwen2.5-7b-32k] [--iters 20]
-    python -m tread_amd.kernel_bench attention [--workload qwen2.5-7b-32k] [--shape recompute|prefill|query]
+    python -m tread_amd.kernel_bench attention [--workload qwen2.5-7b-32k] [--shape recompute|prefill|query] [--sdpa]
     python -m tread_amd.kernel_bench copy      [--workload qwen2.5-7b-32k]
     python -m tread_amd.kernel_bench tiercopy  [--workload qwen2.5-1.5b-16k]
     python -m tread_amd.kernel_bench deviation [--workload qwen2.5-7b-32k]
@@ -10,7 +10,8 @@
 `assemble` launches the fused re-rotate+assemble kernel on one request's blocks (prefix + every
 doc, each doc shifted); `copy` copies the same number of bytes with torch (the calibration for
 HBM traffic counters); `attention` runs the recompute attention kernel on a recompute-shaped row
-set (20% of the doc positions, sorted), a full causal prefill, or the query rows. Each prints its
+set (20% of the doc positions, sorted), a full causal prefill, or the query rows (`--sdpa`: torch's
+scaled_dot_product_attention on the same inputs beside it, the way the reference calls it). Each prints its
 time per launch and achieved GB/s or TFLOP/s; under rocprofv3 every launch is one dispatch.
 `tiercopy` moves every block of a request (prefix + docs) from pinned host memory to the GPU the
 way a batch of host-tier promotions does (layer groups, one library call) and reports the DMA time.
@@ -96,7 +97,7 @@ def bench_tiercopy(cfg, n_docs, doc_len, n_sys, n_query, iters):
           f"{sec * 1e3:.2f} ms, {nbytes / sec / 1e9:.1f} GB/s")
 
 
-def bench_attention(cfg, n_docs, doc_len, n_sys, n_query, iters, shape, ratio=0.2):
+def bench_attention(cfg, n_docs, doc_len, n_sys, n_query, iters, shape, ratio=0.2, sdpa=False):
     hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     T = n_sys + n_docs * doc_len
     g = torch.Generator().manual_seed(0)
@@ -120,6 +121,36 @@ def bench_attention(cfg, n_docs, doc_len, n_sys, n_query, iters, shape, ratio=0.
     flop = 4 * hq * hd * (kend + 1).double().sum().item()
     print(f"attention[{shape}]: rows {n} x {hq} heads over <= {t_cap} keys: {sec * 1e3:.3f} ms, "
           f"{flop / sec / 1e12:.1f} TFLOP/s")
+    if sdpa:
+        _against_sdpa(q, K, V, kend, out, hq, hkv, hd, t_cap, shape, flop, iters)
+
+
+def _against_sdpa(q, K, V, kend, out, hq, hkv, hd, t_cap, shape, flop, iters):
+    """torch's scaled_dot_product_attention on the same inputs, as the reference calls it
+    (tread/blend.py:107-110: K/V expanded to the query heads, a boolean mask key <= row end; the
+    causal prefill shape uses is_causal). Only the flash and memory-efficient backends are tried:
+    the math backend would materialise [heads, rows, keys] scores in bf16."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    n = kend.numel()
+    qh = q.view(1, n, hq, hd).transpose(1, 2).contiguous()
+    kx = K.repeat_interleave(hq // hkv, dim=1).contiguous()
+    vx = V.repeat_interleave(hq // hkv, dim=1).contiguous()
+    causal = shape == "prefill"
+    mask = None if causal else (torch.arange(t_cap, device=kend.device)[None, :] <= kend[:, None])[None, None]
+    mine = out.view(n, hq, hd).transpose(0, 1)
+    for name, backend in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel(backend):
+                fn = lambda: torch.nn.functional.scaled_dot_product_attention(
+                    qh, kx, vx, attn_mask=mask, is_causal=causal, scale=hd ** -0.5)
+                o = fn()
+                torch.cuda.synchronize()
+                diff = (o[0].float() - mine.float()).abs().max().item()
+                sec = _timed(fn, iters)
+            print(f"  torch sdpa[{name}] on the same inputs: {sec * 1e3:.3f} ms, {flop / sec / 1e12:.1f} TFLOP/s, "
+                  f"max |difference| {diff:.2e}")
+        except RuntimeError as e:
+            print(f"  torch sdpa[{name}]: not available ({str(e).splitlines()[0][:120]})")
 
 
 def bench_deviation(cfg, n_docs, doc_len, n_sys, n_query, iters, ratio=0.2):
@@ -182,6 +213,7 @@ def main(argv=None):
     ap.add_argument("--workload", default="qwen2.5-7b-32k", choices=list(WORKLOADS))
     ap.add_argument("--shape", default="recompute", choices=["recompute", "prefill", "query"])
     ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--sdpa", action="store_true", help="attention: also time torch's SDPA on the same inputs")
     args = ap.parse_args(argv)
     name, n_docs, doc_len, n_sys, n_query = WORKLOADS[args.workload]
     cfg = preset(name)
@@ -197,7 +229,7 @@ def main(argv=None):
     elif args.kernel == "deviation":
         bench_deviation(cfg, n_docs, doc_len, n_sys, n_query, args.iters)
     else:
-        bench_attention(cfg, n_docs, doc_len, n_sys, n_query, args.iters, args.shape)
+        bench_attention(cfg, n_docs, doc_len, n_sys, n_query, args.iters, args.shape, sdpa=args.sdpa)
     return 0
 
 
