@@ -388,7 +388,7 @@ def main():
     ap.add_argument("--retune", default=None, metavar="OUT_CSV",
                     help="benchmark GEMM solutions for every shape met (warm-up absorbs it) and write them here")
     ap.add_argument("--gemm-table", default=None, metavar="CSV",
-                    help="GEMM solution table to apply instead of tread_amd/tuning's 7B table")
+                    help="GEMM solution table to apply instead of the model's table in tread_amd/tuning")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU: there is no multi-GPU path (asked for {args.gpus}); "
@@ -398,16 +398,18 @@ def main():
     from tread_amd import BlockStore, Engine, prefill_full
     from tread_amd.model import preset, synthetic_model
 
+    preset_name, n_docs, doc_len, n_sys, n_query = WORKLOADS[args.workload]
     gemm_tables = None
     if not args.no_tune:
-        from tread_amd.tuning import TABLE_7B, use_tuned_gemms
-        table = args.gemm_table or TABLE_7B
-        gemm_tables = use_tuned_gemms(tables=() if args.retune else (table,), tune=bool(args.retune),
-                                      out_file=args.retune)
+        from tread_amd.tuning import table_for, use_tuned_gemms
+        table = args.gemm_table or table_for(preset_name)
+        if table is None:
+            log(f"[bench] no GEMM solution table for {preset_name}: library defaults")
+        tables = () if (args.retune or table is None) else (table,)
+        gemm_tables = use_tuned_gemms(tables=tables, tune=bool(args.retune), out_file=args.retune)
         for t in gemm_tables:
             log(f"[bench] GEMM solution table {t['table']}: {'in effect' if t['loaded'] else 'NOT in effect'}, "
                 f"{t['solutions']} solutions{'; stamps differ: ' + ', '.join(t['mismatched']) if t['mismatched'] else ''}")
-    preset_name, n_docs, doc_len, n_sys, n_query = WORKLOADS[args.workload]
     if args.ratio is None:
         args.ratio = DEFAULT_RATIO.get(args.workload, 0.2)
     cfg = preset(preset_name)
@@ -528,7 +530,7 @@ def main():
                    "doc_len": doc_len, "system": n_sys, "query": n_query, "recompute_ratio": args.ratio,
                    "policy": "deviation", "hipgraph": not args.eager, "query_folded": not args.no_fold,
                    "gemm_tuning": not args.no_tune,
-                   "gemm_table_in_effect": None if gemm_tables is None else all(t["loaded"] for t in gemm_tables),
+                   "gemm_table_in_effect": None if not gemm_tables else all(t["loaded"] for t in gemm_tables),
                    "gpu_tier_docs": n_docs if tier_docs is None else tier_docs, "cold_docs": n_cold,
                    "host_tier_hits_per_request": host_hits, "disk_tier": bool(args.disk_tier),
                    "parallelism": "single GPU"},

@@ -1,11 +1,12 @@
 """GEMM solution tables for the projection GEMMs (hipBLASLt / rocBLAS through PyTorch TunableOp).
 
 The decoder's GEMMs stay plain library GEMMs; TunableOp only chooses, per GEMM shape, which of the
-installed hipBLASLt / rocBLAS solutions runs. `gemm_gfx950_qwen2.5-7b.csv` holds the choices measured
-on MI355X for the 7B-shaped reuse workload (recompute rows at 20 % and 50 % of the doc tokens,
-with and without the 32 query rows riding along, deviation rows, query rows, full-prefill rows);
-TunableOp checks the file's torch / HIP / hipBLASLt / rocBLAS / arch stamps before using it.
-Shapes missing from the table run the library default.
+installed hipBLASLt / rocBLAS solutions runs. `gemm_gfx950_<model>.csv` holds the choices measured
+on MI355X for that model's reuse workload (`bench.py --workload ... --retune`: recompute rows at
+0 %, 20 % and 50 % of the doc tokens, with and without the 32 query rows riding along, deviation
+rows, query rows, full-prefill rows): the 7B 32k, 1.5B 16k and 0.5B 8k workloads. TunableOp
+checks the file's torch / HIP / hipBLASLt / rocBLAS / arch stamps before using it. Shapes missing
+from the table run the library default.
 """
 import os
 import tempfile
@@ -14,6 +15,12 @@ from pathlib import Path
 import torch
 
 TABLE_7B = Path(__file__).resolve().with_name("gemm_gfx950_qwen2.5-7b.csv")
+
+
+def table_for(model_name):
+    """The committed solution table of a model preset (`tread_amd.model.preset` names), or None."""
+    p = Path(__file__).resolve().with_name(f"gemm_gfx950_{model_name}.csv")
+    return p if p.exists() else None
 
 
 def table_validators(path):
