@@ -1140,7 +1140,7 @@ struct SplitPlan {
 };
 
 // Keys per decode_attn work group: at most about DEC_TARGET_WGS work groups over the cache (one
-// per CU: each holds 130 KiB of LDS, so a few more would run as a second round), in whole 32-key
+// per CU: each holds 134 KiB of LDS, so a few more would run as a second round), in whole 32-key
 // tiles, at least two tiles per wave, and at most CMB_MAX_SPLITS slices.
 constexpr int DEC_TARGET_WGS = 256;
 constexpr int DEC_MIN_SPLIT = 2 * DEC_WAVES * DEC_BK;
