@@ -34,8 +34,14 @@ struct AsmSrc {
   int32_t pad;
 };
 
+constexpr int ASM_BUCKETS = 512;
+static_assert(ASM_MAX_SRC < 128, "a bucket entry holds the source index in 7 bits");
+
 struct AsmArgs {
   AsmSrc src[ASM_MAX_SRC];
+  // byte b % 4 of word b / 4: the source of the first unit of work-group bucket b, bit 7 set when
+  // the bucket's units reach into a later source
+  uint32_t bucket_src[ASM_BUCKETS / 4];
   const float* cos_sin;  // [n_src][HD/2][2]: cos, sin of this launch's sources
   bf16_t* dk;
   bf16_t* dv;
@@ -44,8 +50,6 @@ struct AsmArgs {
   int32_t n_kv;
   int32_t layer_lo;
   int32_t n_lr;  // layers in this launch
-  int32_t total_units;
-  int32_t pad;
 };
 
 // Rows per work unit: one 16-byte chunk per thread of one row span (hd 128: K or V; hd 64: the V
@@ -60,14 +64,27 @@ struct AsmUnit {
   int64_t soff;   // element offset of the unit's first row in the source's K (and V)
   int64_t doff;   // element offset of its first destination row in the cache
 };
+// Work group b finds its source through bucket b >> GS of the launch's bucket table: GS is the
+// smallest of ASM_SHIFTS that keeps the grid within ASM_BUCKETS buckets, a template argument of the
+// kernels, so that the bucket word's address depends on the group index alone and its load is the
+// group's first. A binary search over the sources instead took ~6 dependent scalar loads before
+// the group's one 16-byte load per thread could go out (7B request: 646-652 -> 607-609 us).
+constexpr int ASM_SHIFTS[] = {0, 4, 6, 8, 10, 12, 14, 16, 18, 20, 22};
+static int asm_bucket_shift(int64_t groups) {
+  for (int s : ASM_SHIFTS)
+    if (((groups - 1) >> s) < ASM_BUCKETS) return s;
+  return -1;
+}
+
+// The unit's source (the last one whose first unit is <= u: the bucket entry e's source, then, if
+// the bucket reaches into later sources, forward past those that begin at or before u) and its
+// row spans.
 template <int HD>
-__device__ __forceinline__ AsmUnit asm_unit(const AsmArgs& a, int u) {
+__device__ __forceinline__ AsmUnit asm_unit_from(const AsmArgs& a, int u, uint32_t e) {
   constexpr int ROWS = asm_rows<HD>();
-  int lo = 0, hi = a.n_src - 1;  // last source whose first unit is <= u
-  while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if (a.src[mid].unit_begin <= u) lo = mid; else hi = mid - 1;
-  }
+  int lo = e & 0x7f;
+  if (e & 0x80)
+    while (lo + 1 < a.n_src && a.src[lo + 1].unit_begin <= u) ++lo;
   const AsmSrc& src = a.src[lo];
   const int local = u - src.unit_begin;
   const int chunk = local % src.chunks;
@@ -90,14 +107,16 @@ __device__ __forceinline__ uint32_t lane_xor8(uint32_t v) {
 
 // head_dim 128. Work group b is unit b / 2, its K span for even b and its V span for odd b (K
 // only, one group per unit, when the launch moves no V).
+template <int GS>
 __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArgs a) {
   constexpr int HD = 128, HALF = HD / 2, CH = HD / 8;  // 16 chunks per row, 16 rows per unit
-  const bool has_v = a.dv != nullptr;  // uniform: a K-only launch (rotate_keys) moves no V
   const int b = blockIdx.x;
-  const int u = has_v ? b >> 1 : b;
-  if (u >= a.total_units) return;
+  const int bk = b >> GS;  // this group's bucket word: the first load
+  const uint32_t e = (a.bucket_src[bk >> 2] >> ((bk & 3) * 8)) & 0xffu;
+  const bool has_v = a.dv != nullptr;  // uniform: a K-only launch (rotate_keys) moves no V
+  const int u = has_v ? b >> 1 : b;  // the grid holds exactly the launch's (unit, tensor) spans
   const bool is_v = has_v && (b & 1);
-  const AsmUnit w = asm_unit<HD>(a, u);
+  const AsmUnit w = asm_unit_from<HD>(a, u, e);
   const AsmSrc& src = a.src[w.s];
   const int c = threadIdx.x, r = c / CH;
   const bool ok = r < w.rows;
@@ -140,16 +159,16 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArg
 }
 
 // head_dim 64
-template <int HD>
+template <int HD, int GS>
 __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_pairs_kernel(const AsmArgs a) {
   constexpr int HALF = HD / 2;
   constexpr int PG = HALF / 8;               // pair groups per K row
   constexpr int ROWS = asm_rows<HD>();       // 32 (hd 64)
   constexpr int V_PER_T = ROWS * (HD / 8) / ASM_THREADS;  // 16-byte chunks per thread: 1
 
-  const int u = blockIdx.x;
-  if (u >= a.total_units) return;
-  const AsmUnit w = asm_unit<HD>(a, u);
+  const int u = blockIdx.x;  // one group per unit
+  const int bk = u >> GS;
+  const AsmUnit w = asm_unit_from<HD>(a, u, (a.bucket_src[bk >> 2] >> ((bk & 3) * 8)) & 0xffu);
   const int s = w.s, rows = w.rows;
   const int64_t soff = w.soff, doff = w.doff;
   const AsmSrc& src = a.src[s];
@@ -229,6 +248,30 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_pairs_kernel(const 
 
 using namespace tread;
 
+template <int GS>
+static void launch_gs(int head_dim, dim3 grid, dim3 block, hipStream_t s, const AsmArgs& a) {
+  if (head_dim == 128)
+    hipLaunchKernelGGL(rope_assemble_kernel<GS>, grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((rope_assemble_pairs_kernel<64, GS>), grid, block, 0, s, a);
+}
+
+static void launch_assemble(int head_dim, int gs, dim3 grid, dim3 block, hipStream_t s, const AsmArgs& a) {
+  switch (gs) {
+    case 0: launch_gs<0>(head_dim, grid, block, s, a); break;
+    case 4: launch_gs<4>(head_dim, grid, block, s, a); break;
+    case 6: launch_gs<6>(head_dim, grid, block, s, a); break;
+    case 8: launch_gs<8>(head_dim, grid, block, s, a); break;
+    case 10: launch_gs<10>(head_dim, grid, block, s, a); break;
+    case 12: launch_gs<12>(head_dim, grid, block, s, a); break;
+    case 14: launch_gs<14>(head_dim, grid, block, s, a); break;
+    case 16: launch_gs<16>(head_dim, grid, block, s, a); break;
+    case 18: launch_gs<18>(head_dim, grid, block, s, a); break;
+    case 20: launch_gs<20>(head_dim, grid, block, s, a); break;
+    default: launch_gs<22>(head_dim, grid, block, s, a); break;
+  }
+}
+
 extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void* dst_k, void* dst_v,
                                         int n_layers, int n_kv, int64_t t_cap, int head_dim,
                                         const float* cos_sin, int layer_lo, int layer_hi,
@@ -271,6 +314,17 @@ extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void
     }
     if (units == 0) continue;
     if (units > 0x7fffffffLL) return fail(TREAD_ERANGE, "rope_assemble: too many work units");
+    // hd 128: one work group per unit and tensor (K, V)
+    const int64_t groups = head_dim == 128 && dst_v ? 2 * units : units;
+    const int gshift = asm_bucket_shift(groups), ushift = groups == units ? 0 : 1;
+    if (groups > 0x7fffffffLL || gshift < 0) return fail(TREAD_ERANGE, "rope_assemble: too many work units");
+    for (int b = 0, si = 0; b < ASM_BUCKETS; ++b) {  // the units of bucket b's groups
+      const int64_t first = ((int64_t)b << gshift) >> ushift;
+      const int64_t last = ((((int64_t)b + 1) << gshift) - 1) >> ushift;
+      while (si + 1 < cnt && a.src[si + 1].unit_begin <= first) ++si;
+      const bool mixed = si + 1 < cnt && a.src[si + 1].unit_begin <= last;
+      a.bucket_src[b >> 2] |= (uint32_t)(si | (mixed ? 0x80 : 0)) << ((b & 3) * 8);
+    }
     a.n_src = cnt;
     a.cos_sin = cos_sin + (int64_t)base * (head_dim / 2) * 2;
     a.dk = (bf16_t*)dst_k;
@@ -279,15 +333,8 @@ extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void
     a.n_kv = n_kv;
     a.layer_lo = layer_lo;
     a.n_lr = n_lr;
-    a.total_units = (int32_t)units;
-    // hd 128: one work group per unit and tensor (K, V)
-    const int64_t groups = head_dim == 128 && dst_v ? 2 * units : units;
-    if (groups > 0x7fffffffLL) return fail(TREAD_ERANGE, "rope_assemble: too many work units");
     dim3 grid((unsigned)groups), block(ASM_THREADS);
-    if (head_dim == 128)
-      hipLaunchKernelGGL(rope_assemble_kernel, grid, block, 0, (hipStream_t)stream, a);
-    else
-      hipLaunchKernelGGL(rope_assemble_pairs_kernel<64>, grid, block, 0, (hipStream_t)stream, a);
+    launch_assemble(head_dim, gshift, grid, block, (hipStream_t)stream, a);
     int rc = check_launch("rope_assemble");
     if (rc) return rc;
   }
