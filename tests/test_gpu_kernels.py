@@ -109,6 +109,39 @@ def test_rope_assemble_more_sources_than_one_launch_holds(hd):
     assert u.max().item() == 0, (u.max(), (u > 0).sum())
 
 
+@pytest.mark.parametrize("hd,with_v", [(128, True), (64, True), (128, False)])
+def test_rope_assemble_empty_and_uneven_sources(hd, with_v):
+    """Empty, one-token and long sources in one launch: a work group finds its source through the
+    launch's bucket table, and here buckets hold several sources (and empty ones) as well as runs
+    inside one long source. Every source lands rotated in cat order; with no V (rotate_keys' form)
+    only K moves."""
+    g = torch.Generator().manual_seed(13)
+    m = _ref_model(hd)
+    L, kv = 3, 2
+    lens = [0, 1, 0, 3000, 1, 1, 0, 17, 2000, 0, 5, 1, 33, 0]
+    t_cap = sum(lens) + 8
+    srcs, exp_K, exp_V, off = [], [], [], 0
+    for i, n in enumerate(lens):
+        K = (2 * torch.randn(L, 1, kv, n, hd, generator=g)).to(torch.bfloat16)
+        V = torch.randn(L, 1, kv, n, hd, generator=g).to(torch.bfloat16)
+        delta = off + 11 * i - 20
+        srcs.append((K, V, off, delta))
+        exp_K.append(R.rotate_keys_fp32(m, K, delta))
+        exp_V.append(V)
+        off += n
+    dK = torch.zeros(L, 1, kv, t_cap, hd, dtype=torch.bfloat16, device=DEV)
+    dV = torch.zeros_like(dK) if with_v else None
+    _hip.rope_assemble([(K.to(DEV), V.to(DEV) if with_v else None, o, d) for K, V, o, d in srcs], dK, dV,
+                       m.inv_freq)
+    torch.cuda.synchronize()
+    u = bf16_ulps(dK[..., :off, :].cpu(), torch.cat(exp_K, dim=-2))
+    assert u.max().item() == 0, (u.max(), (u > 0).sum())
+    assert (dK[..., off:, :] == 0).all()
+    if with_v:
+        assert torch.equal(dV[..., :off, :].cpu(), torch.cat(exp_V, dim=-2))
+        assert (dV[..., off:, :] == 0).all()
+
+
 def _rotate_fp64(m, K, delta):
     n = K.shape[-2]
     freqs = (m.inv_freq[:, None].float() @ torch.full((1, n), float(delta))).transpose(0, 1).double()

@@ -285,7 +285,8 @@ extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void
     return fail(TREAD_EINVAL, "rope_assemble: layer range [%d,%d) outside [0,%d)", layer_lo, layer_hi, n_layers);
   for (int i = 0; i < n_src; ++i) {
     const tread_src_t& s = srcs[i];
-    if (!s.k || (dst_v && !s.v)) return fail(TREAD_EINVAL, "rope_assemble: source %d has a null pointer", i);
+    if (s.n_tokens > 0 && (!s.k || (dst_v && !s.v)))  // an empty source moves nothing
+      return fail(TREAD_EINVAL, "rope_assemble: source %d has a null pointer", i);
     if (s.n_tokens < 0 || s.dst_off < 0 || s.dst_off + s.n_tokens > t_cap)
       return fail(TREAD_ERANGE, "rope_assemble: source %d rows [%lld,%lld) outside the cache (t_cap %lld)", i,
                   (long long)s.dst_off, (long long)(s.dst_off + s.n_tokens), (long long)t_cap);
