@@ -438,15 +438,16 @@ def subset_attn_scratch(q, k_cache, v_cache, kend, hq, hkv, hd, scale, out, kseg
 # ------------------------------------------------------------------------------------------- (d)
 
 def layer_groups(L):
-    """Layer groups of a tier move, small first (the first layers are needed first): 2, 2, 4, 4, 8,
-    8, ... layers."""
-    groups, a, size = [], 0, 2
+    """Layer groups of a tier move, small first (the first layers are needed first): 1, 1, 2, then
+    4, 4, 8, 8, 16, 16, ... layers. Layer 0 travels alone: a request's deviation pass waits for
+    layer 0 (the prefix rows it attends to) before it starts, and for layer 1 only before its score
+    (1.5B 16k with every block from the host tier: TTFT 21.34-21.69 ms against 21.85-21.89 ms with
+    groups of 2, 2, 4, 4, 8, 8 layers and both waits up front)."""
+    groups, a, n = [], 0, 0
     while a < L:
-        for _ in range(2):
-            if a < L:
-                groups.append((a, min(L, a + size)))
-                a = min(L, a + size)
-        size *= 2
+        size = (1, 1, 2)[n] if n < 3 else 4 << ((n - 3) // 2)
+        groups.append((a, min(L, a + size)))
+        a, n = min(L, a + size), n + 1
     return groups
 
 

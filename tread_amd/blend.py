@@ -179,15 +179,19 @@ def _layer_subset(layer, model, h, S, K, V, inplace=False, ctx=None):
     return (h2 + d)[None], K, V
 
 
-def _deviation(P, ctx_ids, Kl, Vl, all_c):
+def _deviation(P, ctx_ids, Kl, Vl, all_c, hook=None):
     """Layer 0 for all candidates (k/v spliced into layer 0 in place), then layer-1 k/v and the
-    fused deviation score. Returns (score bf16 [n], hidden entering layer 1 [n, H], rows)."""
+    fused deviation score. Returns (score bf16 [n], hidden entering layer 1 [n, H], rows).
+    `hook(1)` runs right before the score reads layer 1 of the cache (its copy may still fly
+    during layer 0)."""
     R = make_rows(P, all_c)
     h, d = layer_forward(P, 0, embed(P, ctx_ids[all_c]), None, R, Kl, Vl)
     lw = P.layers[1]
     h, x = _hip.add_rmsnorm(h, lw.ln1, P.eps, delta=d)
     q_rows = P.hq * P.hd
     kv = F.linear(x, lw.wqkv[q_rows:], None if lw.bqkv is None else lw.bqkv[q_rows:])
+    if hook is not None:
+        hook(1)
     score = _hip.dev_score(kv, R.cos, R.sin, R.rows, P.hkv, P.hd, Kl[1], Vl[1])
     return score, h, R
 
@@ -258,9 +262,8 @@ def _blend(model, ctx_ids, K, V, candidates, ratio, policy, gen, runner, graph, 
         h = embed(P, ctx_ids[S])
     elif policy == "deviation":
         if hook is not None:
-            hook(0)
-            hook(1)
-        score, h_all, _ = _deviation(P, ctx_ids, K, V, all_c)
+            hook(0)  # the prefix rows layer 0 attends to (the doc rows are recomputed in place)
+        score, h_all, _ = _deviation(P, ctx_ids, K, V, all_c, hook=hook)
         sel = _hip.topk_select(score, budget)  # ascending candidate indices => S sorted
         S = all_c[sel]
         h = h_all.index_select(0, sel)

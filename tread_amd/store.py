@@ -4,7 +4,7 @@ Same API, keys, LRU order and statistics as tread/store.py:1-125. A block is the
 for all layers, stacked [layers, 1, kv_heads, tokens, head_dim], plus the position it was computed
 at (`base`). What differs is how bytes move between tiers:
   - a host-tier hit (store.py:73-77) allocates the GPU tensors and queues DMAs from pinned memory
-    on the store's H2D stream in layer groups of growing size (2, 2, 4, 4, 8, 8 layers), one DMA
+    on the store's H2D stream in layer groups of growing size (1, 1, 2, 4, 4, 8, 8 layers), one DMA
     per tensor and group, recording one event per group in `Block.ready` (indexed by layer);
     consumers wait on those events (`Block.wait`) on their own stream, so the copy of layer l
     overlaps whatever runs before layer l is needed. Lookups made inside `batch()` share one
