@@ -90,9 +90,16 @@ class _Assembly:
             if e is not None and id(e) not in self.waited:
                 cur.wait_event(e)
                 self.waited.add(id(e))
+        # the following layers whose copies landed with layer l's (the same event for every pending
+        # block) are assembled by the same launch
+        hi = l + 1
+        while hi < self.P.L and not self.done[hi] and all(
+                b.ready is None or (b.ready[hi] is b.ready[l]) for b, _, _ in self.pending):
+            hi += 1
         self.table = _hip.rope_assemble([(b.K, b.V, off, delta) for b, off, delta in self.pending], self.K, self.V,
-                                        self.P.inv_freq, layer_lo=l, layer_hi=l + 1, table=self.table)
-        self.done[l] = True
+                                        self.P.inv_freq, layer_lo=l, layer_hi=hi, table=self.table)
+        for x in range(l, hi):
+            self.done[x] = True
 
     def finish(self):
         for l in range(self.P.L):
