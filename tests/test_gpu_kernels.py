@@ -261,6 +261,35 @@ def test_skinny_linear_matches_fp32_reference(m, n, k, bias, ldx):
     assert (bf16_ulps(got, ref.to(torch.bfloat16)) == 0).float().mean().item() > 0.95
 
 
+@pytest.mark.parametrize("k", [128, 896, 1536, 2048, 2560, 2816, 3456, 3712, 8960, 13824])
+def test_skinny_row_tail_has_the_bits_of_zero_padding(k):
+    """One row streams each weight row in batches of 7 16-byte chunks per lane (448 per batch); a
+    row of k / 8 chunks that leaves a partial last batch (here 1 .. 7 load steps, some with only
+    part of the lanes in the row) must give the bits of the same row zero-padded to whole batches:
+    the padded products are +0, and a sum that starts at +0 never holds -0, so adding them changes
+    nothing. A dropped chunk or a chunk taken twice in the last batch changes the bits."""
+    g = torch.Generator().manual_seed(k)
+    kp = -(-k // 3584) * 3584
+    n = 96
+    x = torch.randn(1, k, generator=g).to(torch.bfloat16)
+    W = (torch.randn(n, k, generator=g) * 0.05).to(torch.bfloat16)
+    b = torch.randn(n, generator=g).to(torch.bfloat16)
+    xp = torch.zeros(1, kp, dtype=torch.bfloat16)
+    xp[:, :k] = x
+    Wp = torch.zeros(n, kp, dtype=torch.bfloat16)
+    Wp[:, :k] = W
+    got = _hip.skinny_linear(x.to(DEV), W.to(DEV), b.to(DEV))
+    assert torch.equal(got, _hip.skinny_linear(xp.to(DEV), Wp.to(DEV), b.to(DEV)))
+    # the SiLU prologue stages silu(gate) * up, 0 in the padding
+    gu, gup = torch.randn(1, 2 * k, generator=g).to(torch.bfloat16), torch.zeros(1, 2 * kp, dtype=torch.bfloat16)
+    gup[:, :k], gup[:, kp:kp + k] = gu[:, :k], gu[:, k:]
+    assert torch.equal(_hip.skinny_silu_linear(gu.to(DEV), W.to(DEV)), _hip.skinny_silu_linear(gup.to(DEV), Wp.to(DEV)))
+    ref = x.float() @ W.float().T + b.float()  # and the bound of the fp32 reference test above
+    terms = x.float().abs() @ W.float().abs().T + b.float().abs()
+    ulp = 2.0 ** (ref.abs().clamp_min(1e-30).log2().floor() - 7)
+    assert ((got.cpu().float() - ref).abs() <= ulp + 1e-5 * terms).all()
+
+
 def test_skinny_linear_splits_k_for_few_features():
     """Few output features split K over work groups (fp32 partials + a reduce kernel); many do not."""
     assert _hip.lib().tread_skinny_workspace_bytes(8, 3584, 18944) == 4 * 8 * 3584 * 4
