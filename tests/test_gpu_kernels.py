@@ -537,9 +537,11 @@ CASES = [
     # waves of a work group and across work groups (slices merged by the combine kernels), or one
     # slice written directly
     (28, 4, 128, 32098, 1, "query"),   # 7B step over a 32k cache: 63 slices
-    (14, 2, 64, 8100, 1, "query"),     # 0.5B step: 16 slices (few-slice merge)
+    (14, 2, 64, 8100, 1, "query"),     # 0.5B step: 64 slices of 4 tiles (half the waves idle)
+    (12, 2, 128, 16100, 1, "query"),   # 1.5B step: 126 slices, two rounds of the merge's loads
     (64, 8, 128, 33000, 4, "query"),   # 70B, 4 tokens x 8 heads = 32 rows
-    (28, 4, 128, 300, 2, "query"),     # one slice: normalised output written directly
+    (28, 4, 128, 300, 2, "query"),     # 3 slices, the last one of 44 keys
+    (28, 4, 128, 100, 2, "query"),     # one slice: normalised output written directly
     (6, 3, 64, 900, 5, "subset"),      # rows scattered over the cache: per-row key ends mid-tile
     (8, 2, 128, 2000, 4, "segfew"),    # block-diagonal visibility on a few rows
 ]

@@ -59,7 +59,10 @@ def test_error_paths_are_reported_without_a_gpu():
     assert lib.tread_subset_attn_workspace_bytes(32, 28, 4, 128, 32096) > 0
     # one decoding row of a 7B model over 32 096 keys: 63 slices of 512 keys x 4 KV heads x 32 rows
     assert lib.tread_subset_attn_workspace_bytes(1, 28, 4, 128, 32096) == 63 * 4 * 32 * (128 * 4 + 8) + 256
-    assert lib.tread_subset_attn_workspace_bytes(2, 28, 4, 128, 300) == 0  # one slice: no partials
+    # a 0.5B one over 8 100 keys: slices of 4 tiles of 32 keys (few KV heads: 64 x 2 work groups)
+    assert lib.tread_subset_attn_workspace_bytes(1, 14, 2, 64, 8100) == 64 * 2 * 32 * (64 * 4 + 8) + 256
+    assert lib.tread_subset_attn_workspace_bytes(2, 28, 4, 128, 300) == 3 * 4 * 32 * (128 * 4 + 8) + 256
+    assert lib.tread_subset_attn_workspace_bytes(2, 28, 4, 128, 128) == 0  # one slice: no partials
     assert lib.tread_subset_attn_workspace_bytes(6400, 28, 4, 128, 32096) == 2 * 4 * 44 * 256 * (128 * 4 + 8) + 256
     assert lib.tread_subset_attn_workspace_bytes(64, 28, 4, 128, 200) == 0  # 2 row tiles: neither
     assert lib.tread_subset_attn_workspace_bytes(32000, 28, 4, 128, 32096) == 0  # 3 500 work groups: balanced

@@ -1141,9 +1141,13 @@ struct SplitPlan {
 
 // Keys per decode_attn work group: at most about DEC_TARGET_WGS work groups over the cache (one
 // per CU: each holds 134 KiB of LDS, so a few more would run as a second round), in whole 32-key
-// tiles, at least two tiles per wave, and at most CMB_MAX_SPLITS slices.
+// tiles, at least four tiles (half the waves one each), and at most CMB_MAX_SPLITS slices. The
+// floor matters for few KV heads over a short cache: at two tiles per wave a 0.5B-shaped step
+// (2 KV heads, 8k keys) ran 38 work groups and a 1.5B-shaped one (16k keys) 66, each bound by one
+// CU's share of HBM; with four tiles per work group, 130 and 254 (decoding step 0.867 -> 0.834 and
+// 1.454 -> 1.409 ms; one tile per wave: 0.842 and 1.414).
 constexpr int DEC_TARGET_WGS = 256;
-constexpr int DEC_MIN_SPLIT = 2 * DEC_WAVES * DEC_BK;
+constexpr int DEC_MIN_SPLIT = 4 * DEC_BK;
 
 // Row tiles per KV head run as two half-range work groups when there is no key split and the
 // launch is a few rounds of the GPU: a quarter of them (the longest). Simulated dispatch of the
