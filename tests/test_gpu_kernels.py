@@ -241,7 +241,10 @@ def test_silu_mul_vs_torch():
                                              (1, 3584, 18944, True, 18944),
                                              # one row over 16 388 groups of 8 features: 8 passes per
                                              # work group, the last one partial; K of one chunk per lane
-                                             (1, 131104, 128, True, 128)])
+                                             (1, 131104, 128, True, 128),
+                                             # rows shorter than 2 048 over more than 1 024 groups:
+                                             # 2 passes per work group
+                                             (1, 8224, 896, True, 896)])
 def test_skinny_linear_matches_fp32_reference(m, n, k, bias, ldx):
     """y = x W^T (+ b) of a few rows against the fp32 product of the same bf16 values: within one
     bf16 ulp of it plus the fp32 reordering error (1e-5 of the sum of |terms|, which matters only

@@ -401,9 +401,12 @@ void gemv_kernel(const SkinnyArgs a, int rpw) {
 
 // Passes per work group of gemv_kernel (8 rows per pass): one, up to 4 096 work groups, then as
 // few more as keep the launch under that (the prologue is repeated by every work group; 2 048 or
-// 768 work groups measured 3-16 % slower per step, 8 192 the same).
-static int gemv_rpw(int64_t groups) {
-  const int64_t most = 4096;
+// 768 work groups measured 3-16 % slower per step, 8 192 the same). Rows shorter than 2 048 take
+// at most 1 024 work groups: a pass over them is a batch of 2-3 loads per lane, short against the
+// prologue (gate|up of a 0.5B step, 1 216 work groups -> 608 x 2 passes, of a 1.5B step 2 240 ->
+// 560 x 4: decoding step 0.831 -> 0.803 and 1.409 -> 1.375 ms; at most 512: 0.837 and 1.425).
+static int gemv_rpw(int64_t groups, int K) {
+  const int64_t most = K < 2048 ? 1024 : 4096;
   int rpw = 1;
   while (rpw < GV_MAX_RPW && (groups + rpw - 1) / rpw > most) rpw *= 2;
   return rpw;
@@ -411,7 +414,7 @@ static int gemv_rpw(int64_t groups) {
 
 template <int PRO, int EPI>
 static int launch_gemv(int cpt, const SkinnyArgs& a, int64_t groups, hipStream_t s) {
-  const int rpw = gemv_rpw(groups);
+  const int rpw = gemv_rpw(groups, a.K);
   const dim3 grid((unsigned)((groups + rpw - 1) / rpw));
   const size_t lds = (size_t)a.K * sizeof(bf16_t);
   if constexpr (PRO == PRO_NORM) {
