@@ -71,6 +71,7 @@ class _QueryGraph:
         # capture-time positions: the top rows of the bucket, never part of an assembled context
         self.pos = torch.arange(g.t_cap - nq, g.t_cap, dtype=torch.int64, device=device)
         self.last = torch.zeros(1, dtype=torch.int64, device=device)
+        self.last_n = 1  # the query rows `last` was set for (index 0: one row); only `query` writes it
 
         def body():
             R = make_rows(P, self.pos)
@@ -253,7 +254,9 @@ class SubsetRunner:
         if n < q.nq:
             q.ids[n:].zero_()
         torch.arange(T, T + q.nq, out=q.pos)
-        q.last.fill_(n - 1)
+        if q.last_n != n:  # a decoding step keeps n: no fill launch per token
+            q.last.fill_(n - 1)
+            q.last_n = n
         q.graph.replay()
         return q.out
 
