@@ -76,6 +76,8 @@ class _QueryGraph:
         def body():
             R = make_rows(P, self.pos)
             h, d = run_layers(P, embed(P, self.ids), None, R, g.Kl, g.Vl, range(P.L))
+            if nq == 1:  # a decoding step: the one row is the last (a view, no gather launches)
+                return norm_logits(P, h[:1], None if d is None else d[:1])[0]
             return norm_logits(P, h.index_select(0, self.last), d.index_select(0, self.last))[0]
 
         self.graph, self.out = _capture(body, device)
