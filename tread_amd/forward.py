@@ -91,7 +91,9 @@ def layer_forward(P, l, h, delta, R: Rows, K, V, kv_only=False):
 # the norm (or the SiLU gating) fused in front save a launch but redo that prologue in every work
 # group for every row; measured on MI355X they win up to NORM_FUSED_ROWS rows (norm) and
 # SILU_FUSED_ROWS rows (SiLU) and lose beyond (at 8 rows the norm-fused lm_head takes twice the
-# time of RMSNorm + skinny kernel). Fused or not, the results are the same bits.
+# time of RMSNorm + skinny kernel). Fused or not, the results are the same bits. Up to the skinny
+# kernels' 32 rows they lose: a 32-row query forward over a 7B-shaped model's cache of 32k rows
+# took 8.5 ms on them against 6.5 ms on the library GEMMs (the whole request without recompute).
 FEW_ROWS = 8
 NORM_FUSED_ROWS = 2
 SILU_FUSED_ROWS = 4
