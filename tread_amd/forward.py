@@ -93,7 +93,8 @@ def layer_forward(P, l, h, delta, R: Rows, K, V, kv_only=False):
 # SILU_FUSED_ROWS rows (SiLU) and lose beyond (at 8 rows the norm-fused lm_head takes twice the
 # time of RMSNorm + skinny kernel). Fused or not, the results are the same bits. Up to the skinny
 # kernels' 32 rows they lose: a 32-row query forward over a 7B-shaped model's cache of 32k rows
-# took 8.5 ms on them against 6.5 ms on the library GEMMs (the whole request without recompute).
+# took 8.5 ms on them against 6.5 ms on the library GEMMs (the whole request without recompute),
+# over a 0.5B-shaped one's 1k and 8k rows 2.8 and 2.9 ms against 2.2 and 2.4 ms.
 FEW_ROWS = 8
 NORM_FUSED_ROWS = 2
 SILU_FUSED_ROWS = 4
