@@ -452,6 +452,25 @@ def test_decode_within_kl_1e4_at_benchmark_init(name):
         assert kl(b, a) < 1e-4, (i, kl(b, a))
 
 
+def test_graph_decode_of_varying_row_counts_equals_eager(setup):
+    """Decode calls of 3, 4, 3, 2 and 3 tokens on one cache: 3 and 4 share one captured forward of
+    4 padded rows (2 has its own), whose last-row index is refilled only when the row count
+    changes; every call's logits (the last real row's) equal the eager step's."""
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=15)
+    outs = []
+    for graphs in (False, True):
+        eng = Engine(gpu, BlockStore(1 << 30), graphs=graphs)
+        eng.prefill(on(prefix), on(docs), on(query))  # fill the store: the request below hits
+        _, cache, _ = eng.prefill(on(prefix), on(docs), on(query), ratio=0.3, policy="boundary", reserve=16)
+        assert (cache.graph is not None) == graphs
+        g = torch.Generator().manual_seed(15)
+        outs.append([eng.decode(cache, torch.randint(0, cfg.vocab_size, (n,), generator=g).to(DEV))
+                     for n in (3, 4, 3, 2, 3)])
+    for a, b in zip(*outs):
+        assert kl(a, b) < 1e-5
+
+
 def test_graph_decode_equals_eager_decode_and_generate_stops_like_the_reference(setup):
     """The graph step (padded rows) and the eager step give the same logits; Engine.generate's
     stop rules (eos id, max_tokens) cut where tread/server.py:200-206 does, with the same tokens
