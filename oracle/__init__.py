@@ -10,9 +10,11 @@ This package restates, on the CPU with plain PyTorch ops, what the reference com
 
 Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may import it, and
 only to check results (or, for `cpu_baseline`, as the timed CPU path). The product package
-`tread_amd` never imports it and has no CPU fallback.
+`tread_amd` never imports it and has no CPU fallback. Loaded onto a GPU device
+(`model_ref.load(..., device="cuda")`), the same torch code runs there as a second checker, whose
+roundings differ from the CPU's only by the backends' kernels (GEMMs, attention, libm).
 
-How each function is pinned (checks live in tests/test_oracle_*.py):
+How each function is pinned (checks live in tests/test_oracle.py):
 - model math: against transformers' own Qwen2ForCausalLM / LlamaForCausalLM on tiny configs
   (a library routine the reference calls), in fp32.
 - rotate_keys: RoPE group property R(a)R(b) = R(a+b), delta 0 returns the input object,

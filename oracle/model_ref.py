@@ -38,6 +38,10 @@ class RefModel:
     def hd(self):
         return self.cfg.head_dim
 
+    @property
+    def device(self):
+        return self.inv_freq.device
+
     def p(self, name):
         return self.w[name]
 
@@ -48,11 +52,13 @@ def inv_freq_of(cfg):
     return 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.int64).float() / d))
 
 
-def load(cfg, state_dict, dtype=torch.float32):
-    w = {k: v.detach().to("cpu", dtype).clone() for k, v in state_dict.items()}
+def load(cfg, state_dict, dtype=torch.float32, device="cpu"):
+    """Weights as `dtype` on `device`. The oracle normally runs on the CPU; on a GPU device the
+    same torch ops run there (a second backend of the same algorithm, for comparing roundings)."""
+    w = {k: v.detach().to(device, dtype).clone() for k, v in state_dict.items()}
     if "lm_head.weight" not in w:
         w["lm_head.weight"] = w["model.embed_tokens.weight"]
-    return RefModel(cfg=cfg, w=w, dtype=dtype, inv_freq=inv_freq_of(cfg))
+    return RefModel(cfg=cfg, w=w, dtype=dtype, inv_freq=inv_freq_of(cfg).to(device))
 
 
 def rms_norm(x, weight, eps):
@@ -70,6 +76,7 @@ def rope_cos_sin(m: RefModel, pos, dtype):
     pos: LongTensor [n]. Returns cos, sin of shape [1, n, head_dim] (the reference's rotary_emb
     output for a batch of one).
     """
+    pos = pos.to(m.device)
     freqs = (m.inv_freq[:, None].float() @ pos[None, :].float()).transpose(0, 1)
     emb = torch.cat((freqs, freqs), dim=-1)
     return emb.cos().to(dtype)[None], emb.sin().to(dtype)[None]
@@ -117,7 +124,14 @@ def attend(m: RefModel, q, K, V, mask):
     (site:modeling_qwen2.py:186).
     """
     g = m.n_heads // m.n_kv
-    return F.scaled_dot_product_attention(q, repeat_kv(K, g), repeat_kv(V, g), attn_mask=mask)
+    args = (q, repeat_kv(K, g), repeat_kv(V, g))
+    if q.is_cuda:
+        # on a GPU only the memory-efficient kernel (fp32 accumulation, like the CPU kernel): the
+        # math backend's batched bf16 products over transposed views are not used there
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        with sdpa_kernel(SDPBackend.EFFICIENT_ATTENTION):
+            return F.scaled_dot_product_attention(*args, attn_mask=mask)
+    return F.scaled_dot_product_attention(*args, attn_mask=mask)
 
 
 def mlp(m: RefModel, l, x):
@@ -151,12 +165,13 @@ def forward(m: RefModel, ids, past=None, position_ids=None, mask4d=None):
     Returns (h [1, n, hidden] after the final norm, K list, V list) with K/V the full caches.
     """
     n = len(ids)
+    dev = m.device
     P = 0 if past is None else past[0][0].shape[2]
     if position_ids is None:
-        position_ids = torch.arange(P, P + n)
+        position_ids = torch.arange(P, P + n, device=dev)
     cos, sin = rope_cos_sin(m, position_ids, m.dtype)
     if mask4d is None:
-        mask = (torch.arange(P + n)[None, :] <= (P + torch.arange(n))[:, None])[None, None]
+        mask = (torch.arange(P + n, device=dev)[None, :] <= (P + torch.arange(n, device=dev))[:, None])[None, None]
     else:
         mask = mask4d
     h = embed(m, ids)[None]

@@ -3,6 +3,9 @@
 Every function follows the reference op for op (cited file:line under the reference tree), with
 the model math from oracle.model_ref. Runs in fp32 or bf16; in bf16 every torch op rounds where
 the reference's does (e.g. rotate_keys casts cos/sin to bf16 and rounds each product and sum).
+It runs where its model's weights are (oracle.model_ref.load's device; inputs on that device):
+on the CPU as the oracle, or on a GPU as a second backend of the same torch code, whose roundings
+(GEMM kernels, attention kernel, libm) differ from the CPU's.
 """
 import hashlib
 from collections import OrderedDict
@@ -188,7 +191,7 @@ def assemble(m, prefix_ids, docs_ids, mode):
 def subset_ctx(m, S, T, dtype):
     """tread/blend.py:71-79: RoPE for positions S and the bool mask key <= S[i] over T keys."""
     rope = M.rope_cos_sin(m, S, dtype)
-    mask = (torch.arange(T)[None, :] <= S[:, None])[None, None]
+    mask = (torch.arange(T, device=S.device)[None, :] <= S[:, None])[None, None]
     return rope, mask
 
 
@@ -256,16 +259,17 @@ def blend(m, ctx_ids, K, V, candidates, ratio, policy, gen=None, inplace=False, 
         return K, V, all_c[:0], 0.0
     start = 0
     if policy == "boundary":
-        rank = torch.cat([torch.arange(len(c)) for c in candidates])
+        rank = torch.cat([torch.arange(len(c), device=c.device) for c in candidates])
         S = all_c[rank.argsort(stable=True)[:budget]]
     elif policy == "random":
-        S = all_c[torch.randperm(len(all_c), generator=gen)[:budget]]
+        S = all_c[torch.randperm(len(all_c), generator=gen).to(all_c.device)[:budget]]
     elif policy == "deviation":
         dev, h, K[0], V[0], kv1 = layer1_deviation(m, ctx_ids, K, V, all_c, inplace=inplace)
         top = dev.topk(budget).indices
         if trace is not None and trace.get("force_S") is not None:
             where = {int(p): i for i, p in enumerate(all_c.tolist())}
-            top = torch.tensor([where[int(p)] for p in trace["force_S"].tolist()], dtype=torch.long)
+            top = torch.tensor([where[int(p)] for p in trace["force_S"].tolist()], dtype=torch.long,
+                               device=all_c.device)
         if trace is not None:
             trace.update(dev=dev, top=top, all_c=all_c, kv1=kv1)
         S, h, start = all_c[top], h[:, top], 1
@@ -354,13 +358,13 @@ class Engine:
         st.misses += len(miss)
         P = pb.n_tokens
         ids = torch.cat([docs[i] for i in miss])
-        n = len(ids)
-        seg = torch.cat([torch.full((len(docs[i]),), j) for j, i in enumerate(miss)])
-        local = torch.cat([torch.arange(len(docs[i])) for i in miss])
+        n, dev = len(ids), ids.device
+        seg = torch.cat([torch.full((len(docs[i]),), j, device=dev) for j, i in enumerate(miss)])
+        local = torch.cat([torch.arange(len(docs[i]), device=dev) for i in miss])
         st.tokens_prefilled += n
-        allowed = torch.ones(n, P + n, dtype=torch.bool)
+        allowed = torch.ones(n, P + n, dtype=torch.bool, device=dev)
         allowed[:, P:] = (seg[:, None] == seg[None, :]) & (local[:, None] >= local[None, :])
-        mask = torch.zeros(1, 1, n, P + n, dtype=self.m.dtype)
+        mask = torch.zeros(1, 1, n, P + n, dtype=self.m.dtype, device=dev)
         mask.masked_fill_(~allowed, torch.finfo(self.m.dtype).min)
         _, Kl, Vl = M.forward(self.m, ids, past=(list(pb.K.unbind(0)), list(pb.V.unbind(0))),
                               position_ids=P + local, mask4d=mask)
@@ -382,7 +386,7 @@ class Engine:
         for d, b in zip(docs, self.doc_blocks(pkey, pb, docs, st)):
             Ks.append(rotate_keys(self.m, b.K, offset - b.base))
             Vs.append(b.V)
-            cands.append(torch.arange(offset, offset + len(d)))
+            cands.append(torch.arange(offset, offset + len(d), device=prefix_ids.device))
             offset += len(d)
         K = list(torch.cat(Ks, dim=-2).unbind(0))
         V = list(torch.cat(Vs, dim=-2).unbind(0))
@@ -433,7 +437,7 @@ def generate_greedy(m, logits, K, V, max_tokens, eos_ids=(), forced=None):
             reason = "length"
             break
         out.append(nxt)
-        h, K, V = M.forward(m, torch.tensor([nxt]), past=(K, V))
+        h, K, V = M.forward(m, torch.tensor([nxt], device=m.device), past=(K, V))
         logits = M.logits_last(m, h)
         steps.append(logits)
     return out, reason, steps
