@@ -11,10 +11,10 @@ need no CPU oracle run of the whole request:
   on those scores except the choice among exact ties at the threshold; the top-k is sorted,
   distinct, of size k and breaks threshold ties towards the lowest indices;
 - attention on the full recompute shapes (6 400 and 16 000 rows x 28 heads over 32 064 keys)
-  equals fp32 textbook attention on sampled rows;
+  equals float64 attention on sampled rows with planted dominant keys (tests/planted.py);
 - the packed cold prefill of 8 docs at the 70B shape (8 000 rows x 64 heads over 8 064 keys, 8
-  query heads per KV head, block-diagonal visibility) equals per-doc fp32 attention on sampled rows
-  (tread/engine.py:74-95);
+  query heads per KV head, block-diagonal visibility) equals per-doc float64 attention on sampled
+  rows with planted keys (tread/engine.py:74-95);
 - the skinny linear kernel on the vocab-sized lm_head equals the fp32 product.
 """
 import math
@@ -130,54 +130,59 @@ def test_full_deviation_score_and_topk(cfg):
 
 @pytest.mark.parametrize("ratio", [0.2, 0.5])
 def test_full_recompute_attention_on_sampled_rows(cfg, ratio):
+    """The recompute rows of the 7B request (6 400 or 16 000 rows x 28 heads over 32 064 keys:
+    key-half work groups for the longest row tiles, merged by attn_halves_kernel). 64 sampled rows
+    (among them the shortest and the longest) get two planted dominant keys per head
+    (tests/planted.py), so that a dropped or double-counted key half or key tile moves their
+    outputs by O(1), at least 10x the error bound (asserted on the inputs); every sampled row and
+    head is checked against the float64 reference (tread/blend.py:107-110)."""
+    import planted as PL
     hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     T = N_SYS + N_DOCS * DOC_LEN
-    g = torch.Generator(device=DEV).manual_seed(7)
+    g = torch.Generator().manual_seed(7)
+    gd = torch.Generator(device=DEV).manual_seed(7)
     n = int(round(ratio * N_DOCS * DOC_LEN))
-    kend = (torch.randperm(N_DOCS * DOC_LEN, device=DEV, generator=g)[:n].sort().values + N_SYS)
-    q = torch.randn(n, hq, hd, device=DEV, dtype=torch.bfloat16, generator=g)
-    K = torch.randn(1, hkv, T, hd, device=DEV, dtype=torch.bfloat16, generator=g)
-    V = torch.randn_like(K)
-    out = _hip.subset_attn(q, K, V, kend, hq, hkv, hd, hd ** -0.5).view(n, hq, hd)
-    G = hq // hkv
-    rows = torch.randperm(n, device=DEV, generator=g)[:48]
-    rows = torch.cat([rows, torch.tensor([0, n - 1], device=DEV)])  # the shortest and longest rows
-    for r in rows.tolist():
-        e = int(kend[r]) + 1
-        for h in (0, 13, hq - 1):
-            kh = K[0, h // G, :e].float()
-            vh = V[0, h // G, :e].float()
-            p = torch.softmax((kh @ q[r, h].float()) * hd ** -0.5, 0)
-            ref = p @ vh
-            err = (out[r, h].float() - ref).abs().max().item()
-            assert err < 3e-2, (r, h, err)
+    kend = torch.randperm(N_DOCS * DOC_LEN, generator=g)[:n].sort().values + N_SYS
+    q = torch.randn(n, hq, hd, generator=g).to(torch.bfloat16)
+    K = torch.randn(hkv, T, hd, device=DEV, generator=gd).to(torch.bfloat16)
+    V = torch.randn(hkv, T, hd, device=DEV, generator=gd).to(torch.bfloat16)
+    rows = torch.randperm(n, generator=g)[:62].tolist() + [0, n - 1]
+    pairs = [(i, h) for i in rows for h in range(hq)]
+    keys = PL.plant(q, K, kend, pairs, g, per_pair=2)
+    scale = hd ** -0.5
+    out = _hip.subset_attn(q.to(DEV), K[None], V[None], kend.to(DEV), hq, hkv, hd, scale).view(n, hq, hd)
+    ref, mag, drop = PL.reference(q, K, V, kend, pairs, scale, planted=keys)
+    bound, margin = PL.check(torch.stack([out[i, h] for i, h in pairs]), ref, mag, drop, ratio)
+    print(f"\n[7B recompute {n} rows] error bound <= {bound:.3e}; one-key drop effect >= {margin:.1f}x the bound")
 
 
 def test_packed_cold_prefill_attention_at_the_70b_shape():
     """8 cold docs of 1 000 tokens packed on top of a 64-token prefix: row t of doc j sits at cache
-    row P + 1000 j + t and sees the prefix rows [0, P) and its own doc's rows up to itself."""
+    row P + 1000 j + t and sees the prefix rows [0, P) and its own doc's rows up to itself
+    (tread/engine.py:74-95). 44 sampled rows (the first and last of the first two docs among them),
+    every head, two planted dominant keys each within what the row sees (tests/planted.py): a
+    leaked or dropped segment moves their outputs by O(1), at least 10x the error bound."""
+    import planted as PL
     cfg = preset("llama3-70b")
     hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     P, nd, dl = N_SYS, 8, DOC_LEN
     n = nd * dl
-    g = torch.Generator(device=DEV).manual_seed(11)
-    rows = torch.arange(P, P + n, device=DEV)
-    kseg = P + (torch.arange(n, device=DEV) // dl) * dl
-    q = torch.randn(n, hq, hd, device=DEV, dtype=torch.bfloat16, generator=g)
-    K = torch.randn(1, hkv, P + n, hd, device=DEV, dtype=torch.bfloat16, generator=g)
-    V = torch.randn_like(K)
-    out = _hip.subset_attn(q, K, V, rows, hq, hkv, hd, hd ** -0.5, kseg=kseg, n_shared=P).view(n, hq, hd)
-    G = hq // hkv
-    pick = torch.randperm(n, device=DEV, generator=g)[:40].tolist() + [0, dl - 1, dl, n - 1]
-    for i in pick:
-        r, s0 = int(rows[i]), int(kseg[i])
-        keys = torch.cat([torch.arange(P, device=DEV), torch.arange(s0, r + 1, device=DEV)])
-        for h in (0, 9, hq - 1):
-            kh = K[0, h // G, keys].float()
-            vh = V[0, h // G, keys].float()
-            p = torch.softmax((kh @ q[i, h].float()) * hd ** -0.5, 0)
-            err = (out[i, h].float() - p @ vh).abs().max().item()
-            assert err < 3e-2, (i, h, err)
+    g = torch.Generator().manual_seed(11)
+    gd = torch.Generator(device=DEV).manual_seed(11)
+    rows = torch.arange(P, P + n)
+    kseg = P + (torch.arange(n) // dl) * dl
+    q = torch.randn(n, hq, hd, generator=g).to(torch.bfloat16)
+    K = torch.randn(hkv, P + n, hd, device=DEV, generator=gd).to(torch.bfloat16)
+    V = torch.randn(hkv, P + n, hd, device=DEV, generator=gd).to(torch.bfloat16)
+    pick = torch.randperm(n, generator=g)[:40].tolist() + [0, dl - 1, dl, n - 1]
+    pairs = [(i, h) for i in pick for h in range(hq)]
+    keys = PL.plant(q, K, rows, pairs, g, kseg=kseg, n_shared=P, per_pair=2)
+    scale = hd ** -0.5
+    out = _hip.subset_attn(q.to(DEV), K[None], V[None], rows.to(DEV), hq, hkv, hd, scale, kseg=kseg.to(DEV),
+                           n_shared=P).view(n, hq, hd)
+    ref, mag, drop = PL.reference(q, K, V, rows, pairs, scale, kseg=kseg, n_shared=P, planted=keys)
+    bound, margin = PL.check(torch.stack([out[i, h] for i, h in pairs]), ref, mag, drop)
+    print(f"\n[70B packed prefill] error bound <= {bound:.3e}; one-key drop effect >= {margin:.1f}x the bound")
 
 
 @pytest.mark.parametrize("ratio", [0.2, 0.5])

@@ -594,6 +594,53 @@ def test_subset_attention_vs_textbook(hq, hkv, hd, t_cap, n, kind):
     assert err.mean().item() < 3e-3, err.mean()
 
 
+LONG = [
+    # hq, hkv, hd, t_cap, n, kind, planted keys per (row, head)
+    (28, 4, 128, 32098, 1, "query", 3),   # 7B decoding step over a 32k cache: 63 key slices
+    (14, 2, 64, 8100, 1, "query", 3),     # 0.5B step: 64 slices of 4 tiles
+    (12, 2, 128, 16100, 1, "query", 3),   # 1.5B step: 126 slices, two rounds of the merge's loads
+    (64, 8, 128, 33000, 4, "query", 2),   # 70B, 4 tokens x 8 heads = 32 rows per KV head
+    (28, 4, 128, 20000, 32, "query", 2),  # split-K work groups + the many-slice combine
+    (64, 8, 128, 33000, 17, "query", 2),
+    (14, 2, 64, 9000, 5, "query", 2),     # few-slice combine
+    (28, 4, 128, 6000, 40, "subset", 2),  # rows scattered over the cache, split-K
+]
+
+
+@pytest.mark.parametrize("hq,hkv,hd,t_cap,n,kind,per_pair", LONG)
+def test_long_rows_with_planted_keys(hq, hkv, hd, t_cap, n, kind, per_pair):
+    """Rows over long caches, where the kernels split the keys into slices (decode), split-K
+    ranges and merges (tread/blend.py:107-110; tread/engine.py:131-132). Each (row, head) gets
+    `per_pair` keys of dominant score (tests/planted.py), so that dropping or double-counting the
+    key range holding one of them moves the output by O(1) — at least 10x this test's error bound,
+    asserted on the inputs themselves. For a one-row call every 128-key range of the cache holds a
+    planted key of each KV head after the rounds run here; with several rows the rows' strata
+    together cover the cache about as densely (random placement)."""
+    import planted as PL
+    G = hq // hkv
+    g = torch.Generator().manual_seed(hq * 1000 + n + t_cap)
+    gd = torch.Generator(device=DEV).manual_seed(t_cap)
+    if kind == "query":
+        kend = torch.arange(t_cap - n, t_cap)
+    else:
+        kend = torch.sort(torch.randperm(t_cap, generator=g)[:n]).values
+    pairs = [(i, h) for i in range(n) for h in range(hq)]
+    rounds = PL.rounds_for(G * n, per_pair, t_cap)
+    scale = hd ** -0.5
+    bound, margin = 0.0, float("inf")
+    for rnd in range(rounds):
+        q = torch.randn(n, hq, hd, generator=g).to(torch.bfloat16)
+        K = torch.randn(hkv, t_cap, hd, device=DEV, generator=gd).to(torch.bfloat16)
+        V = torch.randn(hkv, t_cap, hd, device=DEV, generator=gd).to(torch.bfloat16)
+        keys = PL.plant(q, K, kend, pairs, g, per_pair=per_pair, rounds=rounds, rnd=rnd)
+        out = _hip.subset_attn(q.to(DEV), K, V, kend.to(DEV), hq, hkv, hd, scale).view(n, hq, hd)
+        ref, mag, drop = PL.reference(q, K, V, kend, pairs, scale, planted=keys)
+        b, m = PL.check(torch.stack([out[i, h] for i, h in pairs]), ref, mag, drop, (rnd, kind, t_cap))
+        bound, margin = max(bound, b), min(margin, m)
+    print(f"\n[{hq}/{hkv}x{hd}, {n} rows over {t_cap} keys, {rounds} rounds] error bound <= {bound:.3e}; "
+          f"one-key drop effect >= {margin:.1f}x the bound")
+
+
 # ------------------------------------------------------------------------------------------- (d)
 
 def test_copy_async_roundtrip_pinned():
