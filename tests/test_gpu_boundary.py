@@ -9,6 +9,8 @@ host-tier promotion.
   only the rows S;
 - `blend(..., runner=SubsetRunner(model))` (tread/blend.py:170-172) replays the captured graph
   (one capture, reused) and gives the eager blend's selection and cache;
+- `SubsetRunner.run(h, S, K, V, start)` in the reference's call form (tread/graphs.py:75-99)
+  equals the eager layer loop;
 - a cache that aliases a graph bucket raises once the next request claims the bucket, and a
   detached copy keeps its rows;
 - rotate_keys moves K only and equals the K of the fused assemble launch;
@@ -130,6 +132,44 @@ def test_blend_uses_the_runner(models, policy, ratio):
         for a, b in zip(Kr + Vr, Ke + Ve):
             assert ((a.float() - b.float()).norm() / b.float().norm()).item() < 1e-2
     assert all(torch.equal(k, k0) for k, k0 in zip(Ks, prefill_kv(gpu, ctx)[0]))  # not inplace
+
+
+def test_runner_run_reference_call_form(models):
+    """SubsetRunner.run(h, S, K, V, start) -> (h, K list, V list) as tread/graphs.py:75-99 defines it
+    and tread/blend.py:170-172 calls it: layers start..L-1 of the sorted positions S replayed from
+    one capture (reused by a second call of the same bucket), equal to the eager loop of
+    _layer_subset over the same layers up to bf16 rounding (the hidden rows after the last layer
+    included), K/V views of the bucket that change exactly the rows S; max_ctx defaults to the
+    reference's 2048."""
+    gpu, _ = models
+    prefix, docs, _ = _request(5)
+    ids = torch.cat([prefix] + docs).to(DEV)
+    T = len(ids)
+    Ks, Vs = prefill_kv(gpu, ids)
+    g = torch.Generator().manual_seed(3)
+    runner = SubsetRunner(gpu)
+    assert runner.max_ctx == 2048 and runner.worth_it(T)
+    for rep, start in enumerate((1, 1, 0)):
+        S = torch.randperm(T - 16, generator=g)[:37].sort().values.to(DEV) + 16
+        h = torch.randn(1, len(S), CFG.hidden_size, generator=g).to(DEV, torch.bfloat16)
+        Kin, Vin = [k.clone() for k in Ks[start:]], [v.clone() for v in Vs[start:]]
+        h_r, K_r, V_r = runner.run(h, S, Kin, Vin, start)
+        assert runner.captures == (1 if rep < 2 else 2), rep
+        assert h_r.shape == h.shape and len(K_r) == len(V_r) == CFG.num_hidden_layers - start
+        assert all(torch.equal(a, b) for a, b in zip(Kin, Ks[start:]))  # the inputs are copied, not written
+        ctx = _subset_ctx(gpu, S, T, h)
+        he, Ke, Ve = h, [k.clone() for k in Ks[start:]], [v.clone() for v in Vs[start:]]
+        for i, l in enumerate(range(start, CFG.num_hidden_layers)):
+            he, Ke[i], Ve[i] = _layer_subset(l, gpu, he, S, Ke[i], Ve[i], inplace=True, ctx=ctx)
+        # the graph runs the bucket's 64 padded rows, the eager loop 37: GEMMs over other row counts
+        # may round differently, so the recomputed values agree to bf16 noise, the rest bit for bit
+        rel = lambda a, b: ((a.float() - b.float()).norm() / b.float().norm()).item()
+        assert rel(h_r, he) < 1e-2, (rep, rel(h_r, he))
+        keep = torch.ones(T, dtype=torch.bool, device=DEV)
+        keep[S] = False
+        for a, b, k0 in zip(K_r + V_r, Ke + Ve, Ks[start:] + Vs[start:]):
+            assert a.shape == b.shape and rel(a[:, :, S], b[:, :, S]) < 1e-2
+            assert torch.equal(a[:, :, keep], k0[:, :, keep])
 
 
 def test_graph_bucket_cache_guard(models):

@@ -330,8 +330,8 @@ def test_eviction_respects_budget(setup):
 @pytest.mark.parametrize("policy,ratio", [("deviation", 0.2), ("boundary", 0.3), ("boundary", 1.0)])
 def test_graph_blend_matches_eager(setup, policy, ratio, fold):
     """tests/test_engine.py:95-113: the hipGraph replay equals the eager loop, and the captured
-    graphs are replayed by the later requests: one capture (the recompute loop, with the query
-    rows folded in, as the reference's count) or two (recompute loop, then the query forward)."""
+    graphs are replayed by the later requests: one recompute-loop capture (the reference's count),
+    plus one query-forward capture when the query rows are not folded in."""
     cfg, gpu, ref = setup
     prefix, docs, query = request(cfg, seed=11)
     eager = Engine(gpu, BlockStore(1 << 30), fold_query=fold)
@@ -343,7 +343,9 @@ def test_graph_blend_matches_eager(setup, policy, ratio, fold):
         b, _, _ = graphed.prefill(on(prefix), on(docs[::-1]), on(query), ratio=ratio, policy=policy)
         assert kl(a, b) < 1e-4
         torch.cuda.synchronize()
-    assert graphed.runner.captures == (1 if fold else 2)
+    # the recompute loop (tread/graphs.py's count); query forwards: the first, ratio-0 request's and,
+    # when not folded, the one beside the recompute loop
+    assert graphed.runner.captures == 1 and graphed.runner.query_captures == (1 if fold else 2)
     if ratio == 1.0:
         full, _, _ = prefill_full(gpu, on(prefix), on(docs[::-1]), on(query))
         assert kl(full, b) < 1e-4
@@ -485,7 +487,9 @@ def test_graph_decode_equals_eager_decode_and_generate_stops_like_the_reference(
     tb, sb, _ = _decode_steps(graphed, prefix, docs, query, 5, 0.3)
     for a, b in zip(sa, sb):
         assert kl(a, b) < 1e-5
-    assert graphed.runner.captures == 2  # recompute loop (query rows folded in), one decode step
+    # the recompute loop (query rows folded in); the first, ratio-0 request's query forward and one
+    # decoding step
+    assert graphed.runner.captures == 1 and graphed.runner.query_captures == 2
     toks, reason, st, cache = eager.generate(on(prefix), on(docs), on(query), max_tokens=5, ratio=0.3,
                                              policy="boundary")
     assert (toks, reason) == (ta, "length") and st.hits == 1 + len(docs)

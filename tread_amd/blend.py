@@ -241,6 +241,27 @@ def blend_query(model, ctx_ids, K, V, candidates, ratio, policy, query_ids, T, g
     return _blend(model, ctx_ids, K, V, candidates, ratio, policy, gen, runner, graph, T, hook, trim_last, query_ids)
 
 
+def _select(P, ctx_ids, K, V, candidates, all_c, budget, policy, gen, hook=None):
+    """The selection of tread/blend.py:144-162: sorted positions S [budget], their hidden rows
+    h [budget, H] entering layer `start` and `start` (1 after the deviation pass, which has
+    recomputed layer 0 of every candidate in place in K[0], V[0])."""
+    dev = all_c.device
+    if policy == "boundary":
+        rank = torch.cat([torch.arange(len(c), device=c.device) for c in candidates])
+        S = all_c[rank.argsort(stable=True)[:budget]].sort().values
+        return S, embed(P, ctx_ids[S]), 0
+    if policy == "random":
+        S = all_c[torch.randperm(len(all_c), generator=gen, device="cpu").to(dev)[:budget]].sort().values
+        return S, embed(P, ctx_ids[S]), 0
+    if policy == "deviation":
+        if hook is not None:
+            hook(0)  # the prefix rows layer 0 attends to (the doc rows are recomputed in place)
+        score, h_all, _ = _deviation(P, ctx_ids, K, V, all_c, hook=hook)
+        sel = _hip.topk_select(score, budget)  # ascending candidate indices => S sorted
+        return all_c[sel], h_all.index_select(0, sel), 1
+    raise ValueError(policy)
+
+
 def _blend(model, ctx_ids, K, V, candidates, ratio, policy, gen, runner, graph, T, hook, trim_last, query_ids):
     P = prepared(model)
     dev = K[0].device
@@ -252,32 +273,16 @@ def _blend(model, ctx_ids, K, V, candidates, ratio, policy, gen, runner, graph, 
         return all_c[:0], 0.0, None
     nq = 0 if query_ids is None else query_ids.numel()
     q_pos = torch.arange(T, T + nq, device=dev) if nq else None
-    start, hq = 0, None
-    if policy == "boundary":
-        rank = torch.cat([torch.arange(len(c), device=c.device) for c in candidates])
-        S = all_c[rank.argsort(stable=True)[:budget]].sort().values
-        h = embed(P, ctx_ids[S])
-    elif policy == "random":
-        S = all_c[torch.randperm(len(all_c), generator=gen, device="cpu").to(dev)[:budget]].sort().values
-        h = embed(P, ctx_ids[S])
-    elif policy == "deviation":
-        if hook is not None:
-            hook(0)  # the prefix rows layer 0 attends to (the doc rows are recomputed in place)
-        score, h_all, _ = _deviation(P, ctx_ids, K, V, all_c, hook=hook)
-        sel = _hip.topk_select(score, budget)  # ascending candidate indices => S sorted
-        S = all_c[sel]
-        h = h_all.index_select(0, sel)
-        if nq:  # the query rows' layer 0 (after every candidate's layer-0 k/v is in place)
-            hq, dq = layer_forward(P, 0, embed(P, query_ids), None, make_rows(P, q_pos), K, V)
-            hq = hq + dq  # the hidden entering layer 1, as the deviation pass returns it
-        start = 1
-    else:
-        raise ValueError(policy)
+    hq = None
+    S, h, start = _select(P, ctx_ids, K, V, candidates, all_c, budget, policy, gen, hook)
+    if nq and start == 1:  # the query rows' layer 0 (after every candidate's layer-0 k/v is in place)
+        hq, dq = layer_forward(P, 0, embed(P, query_ids), None, make_rows(P, q_pos), K, V)
+        hq = hq + dq  # the hidden entering layer 1, as the deviation pass returns it
     if nq and hq is None:
         hq = embed(P, query_ids)
     logits = None
     if graph is not None:
-        out = runner.run(graph, h, S, T, hook=hook, hq=hq)
+        out = runner.replay(graph, h, S, T, hook=hook, hq=hq)
         logits = out if nq else None
     elif nq:
         R = make_rows(P, torch.cat([S, q_pos]))
@@ -296,10 +301,11 @@ def _blend(model, ctx_ids, K, V, candidates, ratio, policy, gen, runner, graph, 
 def blend(model, ctx_ids, K, V, candidates, ratio, policy, gen=None, inplace=False, runner=None):
     """tread/blend.py:133-179 signature: returns (K list, V list, S, eff).
 
-    With a SubsetRunner whose worth_it(T) holds, the recompute layers replay that runner's
-    captured graph: the layers are copied into the bucket's static cache first and back out after
-    (what tread/graphs.py:92-99 does). The engine avoids both copies by assembling straight into
-    the bucket (Engine(graphs=True))."""
+    With a SubsetRunner whose worth_it(T) holds, the selection runs eagerly and the recompute
+    layers go through `runner.run(h, S, K[start:], V[start:], start)`, the reference's call
+    (tread/blend.py:170-172): the layers are copied into the runner's bucket and the returned
+    K[start:], V[start:] are views of it, valid until its next replay, as in the reference. The
+    engine avoids both copies by assembling straight into the bucket (Engine(graphs=True))."""
     K, V = list(K), list(V)
     if not inplace:
         K, V = [k.clone() for k in K], [v.clone() for v in V]
@@ -308,18 +314,12 @@ def blend(model, ctx_ids, K, V, candidates, ratio, policy, gen=None, inplace=Fal
     if runner is None or not candidates or budget == 0 or not runner.worth_it(T):
         S, eff = blend_cache(model, ctx_ids, K, V, candidates, ratio, policy, gen=gen)
         return K, V, S, eff
-    start = 1 if policy == "deviation" else 0
-    with torch.inference_mode():  # the bucket's buffers are inference tensors; K, V stay the caller's kind
-        g = runner.cache_for(start, budget, T, 0, K[0].device)
-        for l in range(len(K)):
-            g.K[l, :, :, :T].copy_(K[l])
-            g.V[l, :, :, :T].copy_(V[l])
-        S, eff = blend_cache(model, ctx_ids, list(g.Kl), list(g.Vl), candidates, ratio, policy, gen=gen,
-                             runner=runner, graph=g, T=T)
-        for l in range(len(K)):
-            K[l].copy_(g.K[l, :, :, :T])
-            V[l].copy_(g.V[l, :, :, :T])
+    P = prepared(model)
+    with torch.inference_mode():  # the bucket's buffers are inference tensors
+        S, h, start = _select(P, ctx_ids, K, V, candidates, torch.cat(candidates), budget, policy, gen)
+        _, K[start:], V[start:] = runner.run(h[None], S, K[start:], V[start:], start)
         S = S.clone()
+    eff = (len(S) * (P.L - start) + start * n) / (n * P.L)
     return K, V, S, eff
 
 

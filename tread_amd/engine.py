@@ -112,8 +112,9 @@ class Engine:
         self.store = store
         self.P = prepared(model)
         # hipGraph replay of the recompute loop (tread/graphs.py); off by default as in the
-        # reference, since each new size bucket pays a one-off capture.
-        self.runner = SubsetRunner(model) if graphs else None
+        # reference, since each new size bucket pays a one-off capture. Requests assemble straight
+        # into a bucket's cache (no copy in or out), so graphs serve every context length.
+        self.runner = SubsetRunner(model, max_ctx=None) if graphs else None
         # with recompute, the query forward rides in the recompute loop (blend_query) instead of
         # running after it: same per-layer inputs, one weight pass less
         self.fold_query = fold_query

@@ -172,9 +172,12 @@ class _QueryBucket:
 
 class SubsetRunner:
     """One captured graph per (start layer, rows bucket, cache bucket, query room); LRU of
-    `max_graphs`. `max_ctx`: contexts above it run eagerly (None: always graph)."""
+    `max_graphs`. `max_ctx`: contexts above it run eagerly (None: always graph). The default is
+    the reference's 2048 (tread/graphs.py:66-70), chosen there because `run` copies the cache into
+    the bucket and back; the engine assembles into its buckets instead, copies nothing, and
+    constructs its runner with max_ctx=None."""
 
-    def __init__(self, model, max_graphs=4, max_ctx=None, trim_last=True, seg=1):
+    def __init__(self, model, max_graphs=4, max_ctx=2048, trim_last=True, seg=1, max_query_buckets=2):
         from tread_amd.blend import prepared
         self.model = model
         self.P = prepared(model)
@@ -183,21 +186,27 @@ class SubsetRunner:
         self.trim_last = trim_last
         self.seg = seg
         self.graphs: "OrderedDict[tuple, _Graph]" = OrderedDict()
+        # buckets of requests that recompute nothing, in an LRU of their own, so that traffic mixing
+        # plain reuse with recompute does not evict (and recapture) recompute buckets; each holds a
+        # full [L, 1, kv, Tb + room, hd] K/V pair (10.8 GB at a 70B shape over 32k tokens)
+        self.max_query_buckets = max_query_buckets
+        self.query_graphs: "OrderedDict[tuple, _QueryBucket]" = OrderedDict()
         self.captures = 0  # graphs of the recompute loop (tread/graphs.py's count, tests/test_engine.py:109)
-        self.query_captures = 0  # query forwards captured for requests that recompute nothing
+        self.query_captures = 0  # query forwards and decoding steps captured over a bucket's cache
 
     def worth_it(self, T):
         return self.max_ctx is None or T <= self.max_ctx
 
-    def _graph(self, start, n, T, n_query, device, nq=0):
+    def _graph(self, start, n, T, n_query, device, nq=0, trim=None):
         nb, Tb = _bucket(n, T)  # the reference's bucket for the recomputed rows, plus the query slots
         nb += nq
-        key = (start, nb, Tb, _q_room(n_query), nq)
+        trim = self.trim_last if trim is None else trim
+        key = (start, nb, Tb, _q_room(n_query), nq, trim)
         g = self.graphs.get(key)
         if g is None:
             while len(self.graphs) >= self.max_graphs:
                 self.graphs.popitem(last=False)
-            g = _Graph(self.P, start, nb, Tb, Tb + key[3], device, self.trim_last, self.seg, nq)
+            g = _Graph(self.P, start, nb, Tb, Tb + key[3], device, trim, self.seg, nq)
             self.graphs[key] = g
             self.captures += 1
         self.graphs.move_to_end(key)
@@ -217,7 +226,7 @@ class SubsetRunner:
             nqb = _q_bucket(n_query)
             if nqb not in g.queries:
                 g.queries[nqb] = _QueryGraph(self.P, g, nqb, device)
-                self.captures += 1
+                self.query_captures += 1
         return g
 
     @torch.inference_mode()
@@ -226,19 +235,19 @@ class SubsetRunner:
         are the cache to assemble into, and the query forward for n_query rows is captured over it
         (before anything is assembled); rows after the context: room >= n_query (for decoding)."""
         Tb = -(-T // t_step) * t_step
-        key = ("query", Tb, _q_room(max(n_query, room or 0)))
-        g = self.graphs.get(key)
+        key = (Tb, _q_room(max(n_query, room or 0)))
+        g = self.query_graphs.get(key)
         if g is None:
-            while len(self.graphs) >= self.max_graphs:
-                self.graphs.popitem(last=False)
-            g = _QueryBucket(self.P, Tb, Tb + key[2], device)
-            self.graphs[key] = g
-        self.graphs.move_to_end(key)
+            while len(self.query_graphs) >= self.max_query_buckets:
+                self.query_graphs.popitem(last=False)
+            g = _QueryBucket(self.P, Tb, Tb + key[1], device)
+            self.query_graphs[key] = g
+        self.query_graphs.move_to_end(key)
         g.generation += 1  # a cache handed out for this bucket earlier is about to be overwritten
         nqb = _q_bucket(n_query)
         if nqb not in g.queries:
             g.queries[nqb] = _QueryGraph(self.P, g, nqb, device)
-            self.query_captures += 1  # not in `captures`, which counts the recompute loop's graphs
+            self.query_captures += 1
         return g
 
     @torch.inference_mode()
@@ -275,11 +284,32 @@ class SubsetRunner:
         nq = _q_bucket(ids.numel())
         if nq not in g.queries:
             g.queries[nq] = _QueryGraph(self.P, g, nq, ids.device)
-            self.captures += 1
+            self.query_captures += 1
         return self.query(g, ids, T)
 
     @torch.inference_mode()
-    def run(self, g, h, S, T, hook=None, hq=None):
+    def run(self, h, S, K, V, start):
+        """tread/graphs.py:75-99, the reference's call form: recompute layers start..L-1 for sorted
+        positions S (len n) with hidden rows h [1, n, H]; K, V are per-layer lists [1, kv, T, hd] for
+        those layers. The layers are copied into the bucket's static cache, its captured loop is
+        replayed (every layer complete, the last one's hidden rows included), and (h [1, n, H] after
+        layer L-1, K list, V list) is returned, K/V being views of the bucket's buffers, valid until
+        the next replay of the same bucket. The engine skips both copies by assembling straight into
+        a bucket (`cache_for`) and replaying it with `replay`."""
+        n, T = len(S), K[0].shape[2]
+        if len(K) != self.P.L - start or len(V) != len(K):
+            raise ValueError(f"run: K/V must hold layers {start}..{self.P.L - 1}")
+        g = self._graph(start, n, T, 0, S.device, trim=False)
+        g.generation += 1  # a cache handed out for this bucket earlier is about to be overwritten
+        for i, (k, v) in enumerate(zip(K, V)):
+            g.K[start + i, :, :, :T].copy_(k)
+            g.V[start + i, :, :, :T].copy_(v)
+        hh, d = self.replay(g, h.reshape(n, -1), S, T)
+        out = (hh[:n] + d[:n])[None]  # the residual add the last layer's output defers
+        return out, list(g.K[start:, :, :, :T].unbind(0)), list(g.V[start:, :, :, :T].unbind(0))
+
+    @torch.inference_mode()
+    def replay(self, g, h, S, T, hook=None, hq=None):
         """Replay layers start..L-1 of bucket graph `g` for sorted positions S (len n) with hidden
         rows h [n, H] over a T-row context, and, for a bucket with query slots, the query rows hq
         [m, H] (m <= g.nq) at positions T, T+1, ...; returns the last query row's logits then
