@@ -121,8 +121,11 @@ int tread_subset_attn_bf16(const void* q, const void* k_cache, const void* v_cac
  * static device array of TREAD_SUBSET_ATTN_SCRATCH_BYTES (128 MiB) that each GPU the library runs
  * on holds until the process ends; its address is looked up on the first call on each device. A
  * shape whose workspace (tread_subset_attn_workspace_bytes) exceeds that size returns TREAD_ERANGE
- * with a message and launches nothing. Every call on one GPU shares that GPU's array: calls that
- * overlap on one GPU (two streams, two threads) race. Same kernels and results as the workspace
+ * with a message and launches nothing. Every call on one GPU shares that GPU's array; calls that
+ * use it are ordered on each GPU: a call on another stream than the previous call's first makes its
+ * stream wait for an event that call recorded (created with the array's address lookup on the first
+ * call per device). Calls on a stream under graph capture neither wait nor record, so a captured
+ * call and calls on other streams that overlap it race. Same kernels and results as the workspace
  * form with a large enough workspace.
  */
 #define TREAD_SUBSET_ATTN_SCRATCH_BYTES (128u << 20)

@@ -3,7 +3,8 @@ C-ABI: on two calls in a row, the second with a smaller input, it gives the same
 tread_subset_attn_bf16 with a workspace of its own, on the shapes whose plans use the partials
 (key halves of the recompute rows, key splits of the query rows, key slices of a decoding step;
 head_dim 128 and 64). A shape whose partials exceed the static array is refused with a message
-before anything is launched.
+before anything is launched. Calls on two streams order themselves (the second waits for the
+first's event), so back-to-back calls without a host synchronisation both give the right bits.
 """
 import pytest
 import torch
@@ -52,6 +53,29 @@ def test_scratch_entry_point_equals_workspace_entry_point(first, second):
         print(f"\n[no-alloc attention] call {i + 1}: {n} rows x {hq} heads over {t_cap} keys, hd {hd}, "
               f"{ws} bytes of partials in the static array")
         assert torch.equal(got, want), (i, (got.float() - want.float()).abs().max().item())
+
+
+def test_scratch_calls_on_two_streams_order_themselves():
+    """Back-to-back calls on two streams with no host synchronisation between them: the second
+    call's stream waits for the event the first recorded, so neither overwrites the other's partials
+    in the shared array (both plans put theirs at its start), and both results equal the workspace
+    entry point's. Repeated with the streams alternating."""
+    big = _case(6432, 28, 4, 128, 32096, seed=31)  # key halves of the 7B recompute rows
+    small = _case(32, 28, 4, 128, 32096, seed=32, sorted_rows=False)  # key splits of its query rows
+    shapes = (28, 4, 128)
+    want = [_hip.subset_attn(q, K, V, kend, *shapes, 128 ** -0.5) for q, K, V, kend in (big, small)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rep in range(3):
+        outs = [torch.full_like(w, 7.0) for w in want]
+        for s in streams:
+            s.wait_stream(torch.cuda.current_stream())
+        for j, (q, K, V, kend) in enumerate((big, small)):
+            with torch.cuda.stream(streams[(j + rep) % 2]):
+                _hip.subset_attn_scratch(q, K, V, kend, *shapes, 128 ** -0.5, outs[j])
+        torch.cuda.synchronize()
+        for j in range(2):
+            assert torch.equal(outs[j], want[j]), (rep, j)
 
 
 def test_scratch_entry_point_refuses_shapes_above_its_array():

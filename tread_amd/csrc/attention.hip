@@ -1274,33 +1274,47 @@ extern "C" int tread_subset_attn_bf16(const void* q, const void* k_cache, const 
 // GPU the library runs on holds until the process ends. Host code never passes the array's name to
 // a kernel (on the host it is only a stand-in): its device address is looked up once per device
 // with hipGetSymbolAddress and kept in g_scratch_ptr. Every call on one GPU shares that GPU's
-// array, so calls that overlap on one GPU race; nothing in it has to start at zero (every partial
-// the merge kernels read is written by the attention kernel of the same call).
+// array; nothing in it has to start at zero (every partial the merge kernels read is written by the
+// attention kernel of the same call). Calls that use the array are ordered among themselves on
+// each GPU: a call on another stream than the previous one first makes its stream wait for the
+// event the previous call recorded after its launches (a host mutex orders the bookkeeping of calls
+// from several threads). Calls on a stream under graph capture neither wait nor record (an event
+// recorded outside the capture cannot be waited on inside it): ordering a captured graph against
+// calls on other streams is the caller's, and such calls that overlap race.
 static __device__ __align__(256) unsigned char scratch[TREAD_SUBSET_ATTN_SCRATCH_BYTES];
 
 namespace {
 constexpr int SCRATCH_MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[SCRATCH_MAX_DEVICES];
+struct ScratchState {
+  void* ptr = nullptr;          // device address of `scratch` on this device
+  hipEvent_t done = nullptr;    // recorded after the last call's launches that used the array
+  hipStream_t stream = nullptr; // that call's stream
+  bool recorded = false;
+};
+ScratchState g_scratch[SCRATCH_MAX_DEVICES];
 }  // namespace
 
-// The current device's address of `scratch`, looked up on the first call on that device.
-static int scratch_for_current_device(void** out) {
+// Set-up on the first call on a device (that device current): the address of `scratch` and the
+// ordering event. Called with g_scratch_mu held.
+static int scratch_state_for_current_device(ScratchState** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail((int)e, "subset_attn_scratch: hipGetDevice: %s", hipGetErrorString(e));
   if (dev < 0 || dev >= SCRATCH_MAX_DEVICES)
     return fail(TREAD_ERANGE, "subset_attn_scratch: device %d outside the %d supported", dev, SCRATCH_MAX_DEVICES);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
+  ScratchState& st = g_scratch[dev];
+  if (!st.ptr) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       return fail(e != hipSuccess ? (int)e : TREAD_EINVAL, "subset_attn_scratch: hipGetSymbolAddress: %s",
                   hipGetErrorString(e));
-    g_scratch_ptr[dev] = p;
+    e = hipEventCreateWithFlags(&st.done, hipEventDisableTiming);
+    if (e != hipSuccess) return fail((int)e, "subset_attn_scratch: hipEventCreate: %s", hipGetErrorString(e));
+    st.ptr = p;
   }
-  *out = g_scratch_ptr[dev];
+  *out = &st;
   return 0;
 }
 
@@ -1317,13 +1331,30 @@ extern "C" int tread_subset_attn_scratch_bf16(const void* q, const void* k_cache
                 "subset_attn_scratch: this shape (n=%lld hq=%d hkv=%d head_dim=%d t_cap=%lld) needs %zu bytes of "
                 "scratch, above the static maximum of %zu; call tread_subset_attn_bf16 with a workspace instead",
                 (long long)n, hq, hkv, head_dim, (long long)t_cap, need, (size_t)TREAD_SUBSET_ATTN_SCRATCH_BYTES);
-  void* ws = nullptr;
-  if (need) {
-    int rc = scratch_for_current_device(&ws);
-    if (rc) return rc;
+  if (!need)  // this plan keeps no partials: the array is not touched
+    return subset_attn_impl(q, k_cache, v_cache, kend, kseg, n_shared, n, hq, hkv, head_dim, t_cap, scale, out,
+                            nullptr, 0, stream);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchState* st = nullptr;
+  int rc = scratch_state_for_current_device(&st);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &cap);
+  if (e != hipSuccess) return fail((int)e, "subset_attn_scratch: hipStreamIsCapturing: %s", hipGetErrorString(e));
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  if (!capturing && st->recorded && st->stream != s) {
+    e = hipStreamWaitEvent(s, st->done, 0);
+    if (e != hipSuccess) return fail((int)e, "subset_attn_scratch: hipStreamWaitEvent: %s", hipGetErrorString(e));
   }
-  return subset_attn_impl(q, k_cache, v_cache, kend, kseg, n_shared, n, hq, hkv, head_dim, t_cap, scale, out, ws,
-                          need ? (size_t)TREAD_SUBSET_ATTN_SCRATCH_BYTES : 0, stream);
+  rc = subset_attn_impl(q, k_cache, v_cache, kend, kseg, n_shared, n, hq, hkv, head_dim, t_cap, scale, out, st->ptr,
+                        (size_t)TREAD_SUBSET_ATTN_SCRATCH_BYTES, stream);
+  if (rc || capturing) return rc;
+  e = hipEventRecord(st->done, s);
+  if (e != hipSuccess) return fail((int)e, "subset_attn_scratch: hipEventRecord: %s", hipGetErrorString(e));
+  st->stream = s;
+  st->recorded = true;
+  return 0;
 }
 
 static int subset_attn_impl(const void* q, const void* k_cache, const void* v_cache, const int64_t* kend,
@@ -1334,7 +1365,8 @@ static int subset_attn_impl(const void* q, const void* k_cache, const void* v_ca
     return fail(TREAD_EINVAL, "subset_attn: bad shape (n=%lld hq=%d hkv=%d)", (long long)n, hq, hkv);
   if (!q || !k_cache || !v_cache || !kend || !out) return fail(TREAD_EINVAL, "subset_attn: null pointer");
   if (head_dim != 64 && head_dim != 128) return fail(TREAD_EINVAL, "subset_attn: head_dim %d not in {64,128}", head_dim);
-  if (t_cap > 0x7fffffffLL - 128) return fail(TREAD_ERANGE, "subset_attn: t_cap too large");
+  // the one-slice decode plan rounds t_cap up to whole 256-key rounds of its waves in an int
+  if (t_cap > 0x7fffffffLL - DEC_WAVES * DEC_BK) return fail(TREAD_ERANGE, "subset_attn: t_cap too large");
   if (n_shared < 0) return fail(TREAD_EINVAL, "subset_attn: negative n_shared");
   if ((((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) & 15) != 0)
     return fail(TREAD_EINVAL, "subset_attn: operands must be 16-byte aligned");
