@@ -27,13 +27,16 @@ HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 # HBM bytes per assemble launch, from two rocprofv3 PMC passes on this workload (FETCH_SIZE x 2.0,
 # WRITE_SIZE x 1.0: the factors a plain copy of known size reads on MI355X); the profiler cannot
-# run inside this process, so the figure is carried here for the workload it was measured on.
-MEASURED_ASSEMBLE_TRAFFIC = {"qwen2.5-7b-32k": 3677613000}
+# run inside this process, so the figure is carried here for the workload it was measured on, with
+# the profile record it comes from (`traffic_source` of the line). Re-measure after a kernel change.
+MEASURED_ASSEMBLE_TRAFFIC = {"qwen2.5-7b-32k": 3677757000}
+ASSEMBLE_TRAFFIC_SOURCE = "profiles/rope_assemble_qwen2.5-7b-32k.md (PMC passes of the current kernel)"
 # HBM bytes per recompute attention call (subset_attn_kernel + attn_halves_kernel), the same two
 # passes and factors on the 6 400-row recompute shape of this workload
 # (`python3 -m tread_amd.kernel_bench attention --shape recompute`): 484.5 + 49.1 MB read,
 # 90.2 + 11.5 MB written
 MEASURED_ATTENTION_TRAFFIC = {"qwen2.5-7b-32k": 635233536}
+ATTENTION_TRAFFIC_SOURCE = "profiles/subset_attn_qwen2.5-7b-32k.md (PMC passes of the current kernel)"
 # doc blocks the GPU tier holds (with the prefix block); the rest spill to the pinned-host tier
 # and are copied back per request on the store's copy streams (None: everything stays on the GPU)
 GPU_TIER_DOCS = {"qwen2.5-1.5b-16k": 8}
@@ -483,6 +486,7 @@ def main():
                     "achieved": round(a_tf, 1), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(a_tf / BF16_MFMA_PEAK_TFLOPS, 4),
                     "traffic": MEASURED_ATTENTION_TRAFFIC.get(args.workload),
+                    "traffic_source": ATTENTION_TRAFFIC_SOURCE if args.workload in MEASURED_ATTENTION_TRAFFIC else None,
                     "avg_us": round(a_sec * 1e6, 2), "algorithmic_flop": a_flop}
         full_ms = full_logits = None
         if args.full_reps > 0:
@@ -541,7 +545,9 @@ def main():
         "gemm_tables": gemm_tables,
         "roofline": {"bound": "hbm", "kernel": "tread::rope_assemble_kernel", "achieved": round(gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": MEASURED_ASSEMBLE_TRAFFIC.get(args.workload), "avg_us": round(sec * 1e6, 2),
+                     "traffic": MEASURED_ASSEMBLE_TRAFFIC.get(args.workload),
+                     "traffic_source": ASSEMBLE_TRAFFIC_SOURCE if args.workload in MEASURED_ASSEMBLE_TRAFFIC else None,
+                     "avg_us": round(sec * 1e6, 2),
                      "algorithmic_bytes": nbytes},
         "roofline_recompute_attention": attn,
         "cpu_baseline": cpu,
