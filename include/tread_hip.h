@@ -118,7 +118,7 @@ int tread_subset_attn_bf16(const void* q, const void* k_cache, const void* v_cac
 /* tread_subset_attn_bf16 without the workspace argument, for callers that cannot allocate device
  * memory (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc). No
  * counterpart in the reference. It calls no allocator: the key-split / key-half partials live in a
- * static device array of TREAD_SUBSET_ATTN_SCRATCH_BYTES (128 MiB) that each GPU the library runs
+ * static device array of TREAD_SUBSET_ATTN_SCRATCH_BYTES (96 MiB) that each GPU the library runs
  * on holds until the process ends; its address is looked up on the first call on each device. A
  * shape whose workspace (tread_subset_attn_workspace_bytes) exceeds that size returns TREAD_ERANGE
  * with a message and launches nothing. Every call on one GPU shares that GPU's array; calls that
@@ -128,7 +128,7 @@ int tread_subset_attn_bf16(const void* q, const void* k_cache, const void* v_cac
  * call and calls on other streams that overlap it race. Same kernels and results as the workspace
  * form with a large enough workspace.
  */
-#define TREAD_SUBSET_ATTN_SCRATCH_BYTES (128u << 20)
+#define TREAD_SUBSET_ATTN_SCRATCH_BYTES (96u << 20)
 int tread_subset_attn_scratch_bf16(const void* q, const void* k_cache, const void* v_cache, const int64_t* kend,
                                    const int64_t* kseg, int64_t n_shared, int64_t n, int hq, int hkv, int head_dim,
                                    int64_t t_cap, float scale, void* out, tread_stream_t stream);

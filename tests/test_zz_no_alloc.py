@@ -79,8 +79,9 @@ def test_scratch_calls_on_two_streams_order_themselves():
 
 
 def test_scratch_entry_point_refuses_shapes_above_its_array():
-    # 1 024 rows x 64 heads (8 KV heads) over 32k keys: key-split partials of ~136 MB
-    n, hq, hkv, hd, t_cap = 1024, 64, 8, 128, 32768
+    # 2 560 rows x 153 heads of their own over 2 560 keys: 10 row tiles per head, the longest 3 in
+    # key halves, partials of ~122 MB
+    n, hq, hkv, hd, t_cap = 2560, 153, 153, 128, 2560
     need = _hip.lib().tread_subset_attn_workspace_bytes(n, hq, hkv, hd, t_cap)
     assert need > _hip.SUBSET_ATTN_SCRATCH_BYTES
     q = torch.zeros(n, hq, hd, device=DEV, dtype=torch.bfloat16)

@@ -411,7 +411,7 @@ def subset_attn(q, k_cache, v_cache, kend, hq, hkv, hd, scale, kseg=None, n_shar
     return out
 
 
-SUBSET_ATTN_SCRATCH_BYTES = 128 << 20  # TREAD_SUBSET_ATTN_SCRATCH_BYTES
+SUBSET_ATTN_SCRATCH_BYTES = 96 << 20  # TREAD_SUBSET_ATTN_SCRATCH_BYTES
 
 
 def subset_attn_scratch(q, k_cache, v_cache, kend, hq, hkv, hd, scale, out, kseg=None, n_shared=0):

@@ -1072,19 +1072,23 @@ __global__ __launch_bounds__(HALF_ROWS * 64) void attn_halves_kernel(const AttnA
   }
 }
 
-// Merge split-K partials of launches with few key slices (nsplit <= CMB_FEW_SPLITS): one wave per
-// (KV head, row), each lane owning HD / 64 output elements, the slices walked in order. Same
-// weights as attn_combine_kernel (exp2(m_s - M), empty slices skipped). One wave per row instead of
-// a 256-thread work group: a 1.5B-shaped recompute (3 232 rows, 12 / 2 heads, 16 096 keys, 4 slices)
-// measured 321 -> 292 us per attention call, a 0.5B-shaped one (1 632 rows, 6 slices) 108 -> 90 us.
+// Merge split-K partials of launches with few key slices (nsplit <= CMB_FEW_SPLITS): HD / 4 lanes
+// per (KV head, row), each owning 4 output elements (one 16-byte load per slice), so a wave merges
+// 64 / (HD / 4) rows; the slices are walked in order. Same weights as attn_combine_kernel
+// (exp2(m_s - M), empty slices skipped). Against one wave per row with HD / 64 elements per lane
+// (4- or 8-byte loads), same bits: a 0.5B-shaped recompute's merge (1 632 rows x 14 heads, 7
+// slices) took 18.0 us, a 1.5B-shaped one (3 232 x 12, 7 slices) 34 us; one wave per row
+// instead of a 256-thread work group had taken a 1.5B-shaped call 321 -> 292 us.
 constexpr int CMB_FEW_SPLITS = 16;
 template <int HD>
 __global__ __launch_bounds__(HALF_ROWS * 64) void attn_combine_few_kernel(const AttnArgs a) {
-  constexpr int EPL = HD / 64;  // elements per lane
+  constexpr int LPR = HD / 4;    // lanes per row, 4 elements each
+  constexpr int RPW = 64 / LPR;  // rows per wave
   const int lane = threadIdx.x & 63;
+  const int q4 = lane % LPR;
   const int64_t R = a.n * a.G;
-  const int64_t w = (int64_t)blockIdx.x * HALF_ROWS + (threadIdx.x >> 6);
-  if (w >= (int64_t)a.hkv * R) return;
+  const int64_t w = ((int64_t)blockIdx.x * HALF_ROWS + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  if (w >= (int64_t)a.hkv * R) return;  // lanes work alone: no cross-lane operation below
   const int head = (int)(w / R);
   const int64_t r = w % R;
   const int tile = (int)(r / a.prow), in_tile = (int)(r % a.prow);
@@ -1092,7 +1096,8 @@ __global__ __launch_bounds__(HALF_ROWS * 64) void attn_combine_few_kernel(const 
   const int64_t p0 = ((int64_t)head * a.tiles + tile) * a.prow + in_tile;
   // every slice's (max, sum) and partial O are loaded up front (one round of memory latency, not
   // one per slice); the merge then walks the slices in order
-  float mv[CMB_FEW_SPLITS], lv[CMB_FEW_SPLITS], ov[CMB_FEW_SPLITS][EPL];
+  float mv[CMB_FEW_SPLITS], lv[CMB_FEW_SPLITS];
+  f32x4_t ov[CMB_FEW_SPLITS];
 #pragma unroll
   for (int sp = 0; sp < CMB_FEW_SPLITS; ++sp) {
     if (sp < a.nsplit) {
@@ -1100,36 +1105,30 @@ __global__ __launch_bounds__(HALF_ROWS * 64) void attn_combine_few_kernel(const 
       const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + p * 2);
       mv[sp] = ml.x;
       lv[sp] = ml.y;
-      const float* o = a.ws_o + p * HD + lane * EPL;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) ov[sp][e] = o[e];
+      ov[sp] = *reinterpret_cast<const f32x4_t*>(a.ws_o + p * HD + q4 * 4);
     }
   }
   float M = -INFINITY;
 #pragma unroll
   for (int sp = 0; sp < CMB_FEW_SPLITS; ++sp)
     if (sp < a.nsplit && lv[sp] > 0.f) M = fmaxf(M, mv[sp]);
-  float L = 0.f, acc[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+  float L = 0.f;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int sp = 0; sp < CMB_FEW_SPLITS; ++sp) {
     if (sp < a.nsplit && lv[sp] > 0.f) {
       const float wgt = __builtin_amdgcn_exp2f(mv[sp] - M);
       L += wgt * lv[sp];
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[e] += wgt * ov[sp][e];
+      for (int e = 0; e < 4; ++e) acc[e] += wgt * ov[sp][e];
     }
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   const int64_t qi = r / a.G;
   const int qh = head * a.G + (int)(r % a.G);
-  bf16_t* op = a.out + (qi * a.hq + qh) * HD + lane * EPL;
-  if constexpr (EPL == 2) {
-    *reinterpret_cast<uint32_t*>(op) = pack_bf(acc[0] * inv, acc[1] * inv);
-  } else {
-    op[0] = f2bf(acc[0] * inv);
-  }
+  bf16_t* op = a.out + (qi * a.hq + qh) * HD + q4 * 4;
+  const u32x2_t o2 = {pack_bf(acc[0] * inv, acc[1] * inv), pack_bf(acc[2] * inv, acc[3] * inv)};
+  *reinterpret_cast<u32x2_t*>(op) = o2;
 }
 
 struct SplitPlan {
@@ -1160,6 +1159,21 @@ constexpr int DEC_MIN_SPLIT = 4 * DEC_BK;
 constexpr int ATT_LONG_MIN_TILES = 8;
 constexpr int64_t ATT_LONG_MAX_WGS = 1536;
 
+// Compute units of the current device, looked up once per device.
+static int cu_count() {
+  static std::mutex mu;
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cache[dev]) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cache[dev] = v;
+  }
+  return cache[dev];
+}
+
 static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
   SplitPlan sp;
   sp.decode = false;
@@ -1182,12 +1196,22 @@ static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
   sp.split_len = 0;
   sp.nlong = 0;
   if (base < ATT_TARGET_WGS && t_cap >= 2 * ATT_MIN_SPLIT_KEYS) {
-    // Launches of many row tiles (ragged key ranges when rows are sorted by position) aim at twice
-    // the work groups in slices of at least twice the keys: a 1.5B-shaped recompute (152 row-tile
-    // groups, 16 096 keys) measured 300 -> 248 us with 7 slices instead of 4; slices of 704 keys
-    // (12 over 8 096) measured slower than 6.
     const bool many = base >= ATT_MANY_TILE_WGS;
-    int64_t want = ((many ? 2 * ATT_TARGET_WGS : ATT_TARGET_WGS) + base - 1) / base;
+    int64_t want = (ATT_TARGET_WGS + base - 1) / base;
+    if (many) {
+      // Many row tiles with ragged key ranges (recompute rows sorted by position): about three
+      // work groups per CU over the launch, rounded, skipping multiples of 4; none when the row
+      // tiles alone fill the CUs (then whole tiles, the longest in key halves). Swept in whole
+      // requests on MI355X (deviation-selected rows, graph buckets, TTFT in one process): 0.5B 8k
+      // (100 row-tile groups) 8.10 / 7.01 / 6.46 / 6.36 / 6.28 / 6.45 / 6.43 ms with 2 / 3 / 5 /
+      // 6 / 7 / 9 / 11 slices, 1.5B 16k (158 groups) 21.76 / 19.63 / 19.42 / 19.94 / 19.74 /
+      // 19.95 ms with 2 / 3 / 5 / 6 / 7 / 9; slice counts that are multiples of 4 were slow on
+      // every shape swept. The 0.5B deviation pass (438 groups) ran 245 us in 3 slices and 201 us
+      // in whole tiles with key halves.
+      const int64_t cus = cu_count();
+      want = base >= cus ? 1 : (6 * cus / base + 1) / 2;
+      if (want >= 4 && want % 4 == 0) --want;
+    }
     int64_t most = t_cap / (many ? 2 * ATT_MIN_SPLIT_KEYS : ATT_MIN_SPLIT_KEYS);
     int64_t ns = want < most ? want : most;
     if (ns > CMB_MAX_SPLITS) ns = CMB_MAX_SPLITS;
@@ -1226,7 +1250,8 @@ static int subset_attn_impl(const void* q, const void* k_cache, const void* v_ca
 static int launch_combine(const AttnArgs& a, int head_dim, hipStream_t s) {
   const int64_t blocks = (int64_t)a.hkv * a.n * a.G;
   if (a.nsplit <= CMB_FEW_SPLITS) {
-    const dim3 fgrid((unsigned)((blocks + HALF_ROWS - 1) / HALF_ROWS));
+    const int64_t rows_per_wg = (int64_t)HALF_ROWS * (64 / (head_dim / 4));
+    const dim3 fgrid((unsigned)((blocks + rows_per_wg - 1) / rows_per_wg));
     if (head_dim == 128)
       hipLaunchKernelGGL(attn_combine_few_kernel<128>, fgrid, dim3(HALF_ROWS * 64), 0, s, a);
     else
