@@ -40,7 +40,10 @@ namespace tread {
 constexpr int ATT_WAVES = 8;
 constexpr int ATT_THREADS = ATT_WAVES * 64;
 constexpr int ATT_BM = ATT_WAVES * 32;         // rows per work group (32 per wave)
-constexpr int ATT_BK = 64;                     // keys per tile
+// keys per pipeline step: 64 at head_dim 128; 128 at head_dim 64, whose steps have half the MFMA
+// work per key, so that a step's fixed costs (barrier, first fragment latencies, tile bookkeeping)
+// are spread over the same MFMA work and the same LDS tile bytes as at head_dim 128
+constexpr int att_bk(int head_dim) { return head_dim == 64 ? 128 : 64; }
 constexpr int ATT_NBUF = 3;                    // LDS tile buffers (software pipeline depth)
 constexpr int N_XCD = 8;
 constexpr int ATT_TARGET_WGS = 512;     // split-K when fewer (head, row tile) work groups than this
@@ -63,7 +66,7 @@ struct AttnArgs {
   int32_t tiles;  // row tiles per KV head
   int32_t xpg;    // XCDs per KV head (0: plain mapping)
   int32_t nsplit;
-  int32_t split_len;  // keys per split (multiple of ATT_BK)
+  int32_t split_len;  // keys per split (multiple of att_bk(HD))
   int32_t nlong;      // (nsplit 1) the nlong longest row tiles per KV head run as two work groups
   int32_t prow;       // rows per row tile in the split-K partials (ATT_BM; DEC_ROWS for decode_attn)
   float scale_log2;
@@ -79,8 +82,9 @@ struct AttnArgs {
 template <int HD>
 struct AttnSmem {
   static constexpr int NCH = HD / 8;  // 16-byte chunks per row
-  static constexpr int K_ELEMS = ATT_BK * HD;
-  static constexpr int V_ELEMS = ATT_BK * HD;
+  static constexpr int BK = att_bk(HD);
+  static constexpr int K_ELEMS = BK * HD;
+  static constexpr int V_ELEMS = BK * HD;
   static constexpr int BUF = K_ELEMS + V_ELEMS;
   static __device__ __forceinline__ int k_swz(int r) { return r & (NCH - 1); }
   static __device__ __forceinline__ int v_swz(int r) {
@@ -196,10 +200,13 @@ __device__ __forceinline__ float xhalf_sum(float v) {
 template <int HD>
 __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs a) {
   using SM = AttnSmem<HD>;
+  constexpr int BK = SM::BK;    // keys per tile
+  constexpr int NKB = BK / 32;  // 32-key blocks of a tile (score MFMA blocks)
+  constexpr int NST = BK / 16;  // k-steps of the PV product
   constexpr int KS = HD / 16;   // k-steps of the QK product
   constexpr int DB = HD / 32;   // 32-row d blocks of O^T
   constexpr int KCH = HD / 8;   // 16-byte chunks per K/V row
-  constexpr int K_LD = ATT_BK * KCH / ATT_THREADS;  // K (and V) 16-byte chunks per thread per tile
+  constexpr int K_LD = BK * KCH / ATT_THREADS;  // K (and V) 16-byte chunks per thread per tile
   extern __shared__ __align__(16) bf16_t smem[];
   __shared__ int red[4][ATT_WAVES];
 
@@ -282,8 +289,8 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     startB = max(startB, lo);
     endB = min(endB, hi);
   }
-  const int nA = endA > startA ? (endA - startA + ATT_BK - 1) / ATT_BK : 0;
-  const int nB = endB > startB ? (endB - startB + ATT_BK - 1) / ATT_BK : 0;
+  const int nA = endA > startA ? (endA - startA + BK - 1) / BK : 0;
+  const int nB = endB > startB ? (endB - startB + BK - 1) / BK : 0;
   // this work group's key tiles [jbase, jbase + ntiles) of the nA + nB (a half for kpart 0 / 1)
   int jbase = 0, ntiles = nA + nB;
   if (kpart >= 0) {
@@ -328,11 +335,11 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   auto tile_bounds = [&](int jl, int& s0, int& s1) {
     const int j = jbase + jl;
     if (j < nA) {
-      s0 = startA + j * ATT_BK;
-      s1 = min(s0 + ATT_BK, endA);
+      s0 = startA + j * BK;
+      s1 = min(s0 + BK, endA);
     } else {
-      s0 = startB + (j - nA) * ATT_BK;
-      s1 = min(s0 + ATT_BK, endB);
+      s0 = startB + (j - nA) * BK;
+      s1 = min(s0 + BK, endB);
     }
   };
   // Queue tile j's K and V rows straight into LDS buffer `buf`, one wave-wide 16-byte load at a
@@ -383,7 +390,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   uint32_t kaddr[KS];
 #pragma unroll
   for (int st = 0; st < KS; ++st) kaddr[st] = lds_addr(smem + c * HD + ((2 * st + half) ^ SM::k_swz(c)) * 8);
-  constexpr int NK = 2 * KS;  // K fragments per tile
+  constexpr int NK = NKB * KS;  // K fragments per tile
   constexpr int RING = 4;     // K fragment reads in flight ahead of the MFMAs
   constexpr int NV = 2 * DB;  // transposing reads per PV k-step
 
@@ -398,7 +405,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   };
   // S^T = K Q^T for the tile in buffer `buf`: s[kb] holds keys kb * 32 + (x / 4) * 8 + half * 4 + x % 4
   // (register x) of this lane's query column. K fragments stream RING reads ahead of the MFMAs.
-  auto qk = [&](int buf, f32x16_t (&s)[2]) {
+  auto qk = [&](int buf, f32x16_t (&s)[NKB]) {
     const uint32_t ko = (uint32_t)(buf * SM::BUF * 2);
     bf16x8_t kf[NK];
     static_for<RING>([&](auto I) {
@@ -425,14 +432,14 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   // the scores arrive relative to a stale max m_run and move (with O and the sums) only when some
   // row's max outgrew it by more than 2^8, or on a row's first visible keys; p then stays <= 256
   // and the final division by the sum is exact either way
-  auto settle = [&](int j, f32x16_t (&s)[2]) {
+  auto settle = [&](int j, f32x16_t (&s)[NKB]) {
     int s0, s1;
     tile_bounds(j, s0, s1);
-    const bool full = (s1 - s0 == ATT_BK) && (s1 - 1 <= kmin) && (jbase + j < nA || s0 >= segmax);
+    const bool full = (s1 - s0 == BK) && (s1 - 1 <= kmin) && (jbase + j < nA || s0 >= segmax);
     if (!full) {
       asm volatile("");  // keeps this rare path a branch: no speculated predicates on full tiles
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int x = 0; x < 16; ++x) {
           const int key = s0 + kb * 32 + (x >> 2) * 8 + half * 4 + (x & 3);
@@ -444,9 +451,12 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       mx[q] = fmaxf(fmaxf(s[0][q], s[0][q + 4]), s[0][q + 8]);
-      mx[q] = fmaxf(fmaxf(mx[q], s[0][q + 12]), s[1][q]);
-      mx[q] = fmaxf(fmaxf(mx[q], s[1][q + 4]), s[1][q + 8]);
-      mx[q] = fmaxf(mx[q], s[1][q + 12]);
+      mx[q] = fmaxf(mx[q], s[0][q + 12]);
+#pragma unroll
+      for (int kb = 1; kb < NKB; ++kb) {
+        mx[q] = fmaxf(fmaxf(mx[q], s[kb][q]), s[kb][q + 4]);
+        mx[q] = fmaxf(fmaxf(mx[q], s[kb][q + 8]), s[kb][q + 12]);
+      }
     }
     const float tmax = xhalf_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])));
     const bool need = m_set ? tmax > ATT_RESCALE_LOG2 : tmax > -INFINITY;
@@ -460,7 +470,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
 #pragma unroll
         for (int x = 0; x < 16; ++x) oacc[d][x] *= corr;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int x = 0; x < 16; ++x) s[kb][x] -= sh;
       m_run += sh;
@@ -469,11 +479,11 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       for (int x = 0; x < 16; ++x) mneg[x] = -m_run;
     }
   };
-  // P = exp2(S') (S' = s * scale * log2(e) - m) as the B operand of the 4 PV k-steps (16 keys
+  // P = exp2(S') (S' = s * scale * log2(e) - m) as the B operand of the NST PV k-steps (16 keys
   // each); register x of s[kb] feeds k-step kb * 2 + x / 8
-  auto to_p = [&](f32x16_t (&s)[2], bf16x8_t (&pb)[4]) {
+  auto to_p = [&](f32x16_t (&s)[NKB], bf16x8_t (&pb)[NST]) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int x = 0; x < 16; ++x) {
         const float p = __builtin_amdgcn_exp2f(s[kb][x]);
@@ -481,7 +491,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
         lsum[x & 3] += p;
       }
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
         u32x4_t pw;
@@ -493,9 +503,9 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   // O^T += V^T P^T over the tile in buffer `buf`: k-step st covers tile keys st * 16 + half * 4 +
   // (0..3) and st * 16 + 8 + half * 4 + (0..3); fragment reads run one k-step ahead of the MFMAs.
   // v0 holds k-step 0's fragments, already queued.
-  auto pv = [&](int buf, const bf16x8_t (&pb)[4], s16x4_t (&v0)[NV]) {
+  auto pv = [&](int buf, const bf16x8_t (&pb)[NST], s16x4_t (&v0)[NV]) {
     const uint32_t off = (uint32_t)(buf * SM::BUF * 2);
-    s16x4_t v1[NV], v2[NV], v3[NV];
+    s16x4_t v1[NV];
     auto mm = [&](const s16x4_t (&f)[NV], const bf16x8_t& p) {
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
@@ -503,17 +513,20 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
         oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, p, oacc[d], 0, 0, 0);
       }
     };
-    v_read(std::integral_constant<int, 1>{}, off, v1);
-    lgkm_wait<NV>(v0);
-    mm(v0, pb[0]);
-    v_read(std::integral_constant<int, 2>{}, off, v2);
-    lgkm_wait<NV>(v1);
-    mm(v1, pb[1]);
-    v_read(std::integral_constant<int, 3>{}, off, v3);
-    lgkm_wait<NV>(v2);
-    mm(v2, pb[2]);
-    lgkm_wait<0>(v3);
-    mm(v3, pb[3]);
+    // k-steps alternate between the fragment sets v0 and v1: the next step's reads are queued
+    // (NV LDS reads) before this step's fragments are waited for
+    static_for<NST>([&](auto I) {
+      constexpr int st = decltype(I)::value;
+      s16x4_t(&cur)[NV] = (st & 1) ? v1 : v0;
+      s16x4_t(&nxt)[NV] = (st & 1) ? v0 : v1;
+      if constexpr (st + 1 < NST) {
+        v_read(std::integral_constant<int, st + 1>{}, off, nxt);
+        lgkm_wait<NV>(cur);
+      } else {
+        lgkm_wait<0>(cur);
+      }
+      mm(cur, pb[st]);
+    });
   };
 
   // Software pipeline over tiles with ATT_NBUF LDS buffers (tile t in buffer t % ATT_NBUF): the
@@ -573,8 +586,8 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     }
     tile_barrier();
     const bool late = wv >= ATT_WAVES / 2;
-    f32x16_t sc[2];
-    bf16x8_t pb[4];
+    f32x16_t sc[NKB];
+    bf16x8_t pb[NST];
     qk(0, sc);
     int j = 0, bj = 0;  // bj = j % ATT_NBUF
     if (!late) {
@@ -1174,7 +1187,7 @@ static int cu_count() {
   return cache[dev];
 }
 
-static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
+static SplitPlan plan_split(int64_t n, int hq, int hkv, int head_dim, int64_t t_cap) {
   SplitPlan sp;
   sp.decode = false;
   if (n * (hq / hkv) <= DEC_ROWS) {
@@ -1217,7 +1230,8 @@ static SplitPlan plan_split(int64_t n, int hq, int hkv, int64_t t_cap) {
     if (ns > CMB_MAX_SPLITS) ns = CMB_MAX_SPLITS;
     if (ns > 1) {
       int64_t len = (t_cap + ns - 1) / ns;
-      len = (len + ATT_BK - 1) / ATT_BK * ATT_BK;
+      const int64_t bk = att_bk(head_dim);
+      len = (len + bk - 1) / bk * bk;
       sp.nsplit = (int)((t_cap + len - 1) / len);
       sp.split_len = (int)len;
     }
@@ -1282,7 +1296,7 @@ static int decode_attn_launch(AttnArgs& a, const SplitPlan& sp, int head_dim, hi
 
 extern "C" size_t tread_subset_attn_workspace_bytes(int64_t n, int hq, int hkv, int head_dim, int64_t t_cap) {
   if (n <= 0 || hq <= 0 || hkv <= 0 || (hq % hkv) != 0 || t_cap <= 0) return 0;
-  return split_ws_bytes(plan_split(n, hq, hkv, t_cap), hkv, head_dim);
+  return split_ws_bytes(plan_split(n, hq, hkv, head_dim, t_cap), hkv, head_dim);
 }
 
 extern "C" int tread_subset_attn_bf16(const void* q, const void* k_cache, const void* v_cache, const int64_t* kend,
@@ -1350,7 +1364,7 @@ extern "C" int tread_subset_attn_scratch_bf16(const void* q, const void* k_cache
   if (n == 0) return 0;
   if (n < 0 || hq <= 0 || hkv <= 0 || (hq % hkv) != 0 || t_cap <= 0)
     return fail(TREAD_EINVAL, "subset_attn_scratch: bad shape (n=%lld hq=%d hkv=%d)", (long long)n, hq, hkv);
-  const size_t need = split_ws_bytes(plan_split(n, hq, hkv, t_cap), hkv, head_dim);
+  const size_t need = split_ws_bytes(plan_split(n, hq, hkv, head_dim, t_cap), hkv, head_dim);
   if (need > (size_t)TREAD_SUBSET_ATTN_SCRATCH_BYTES)
     return fail(TREAD_ERANGE,
                 "subset_attn_scratch: this shape (n=%lld hq=%d hkv=%d head_dim=%d t_cap=%lld) needs %zu bytes of "
@@ -1409,7 +1423,7 @@ static int subset_attn_impl(const void* q, const void* k_cache, const void* v_ca
   a.hq = hq;
   a.hkv = hkv;
   a.G = hq / hkv;
-  SplitPlan sp = plan_split(n, hq, hkv, t_cap);
+  SplitPlan sp = plan_split(n, hq, hkv, head_dim, t_cap);
   const size_t need = split_ws_bytes(sp, hkv, head_dim);
   if (need && (!ws || ws_bytes < need)) {  // no workspace: one pass per row tile (decode: one slice)
     sp.nsplit = 1;
