@@ -6,6 +6,7 @@
     python -m tread_amd.kernel_bench tiercopy  [--workload qwen2.5-1.5b-16k]
     python -m tread_amd.kernel_bench deviation [--workload qwen2.5-7b-32k]
     python -m tread_amd.kernel_bench skinny    [--workload qwen2.5-7b-32k]
+    python -m tread_amd.kernel_bench request   [--workload qwen2.5-7b-32k] [--libs a.so,b.so]
 
 `assemble` launches the fused re-rotate+assemble kernel on one request's blocks (prefix + every
 doc, each doc shifted); `copy` copies the same number of bytes with torch (the calibration for
@@ -19,7 +20,9 @@ way a batch of host-tier promotions does (layer groups, one library call) and re
 against the assembled layer-1 cache) and selects the top 20% of them, each launch timed alone.
 `skinny` runs the projections of a decoding step (q|k|v with bias, o, gate|up, down, lm_head) for
 1, 8 and 32 token rows through the skinny-linear kernel and through torch's GEMM, and reports the
-weight-streaming bandwidth of each.
+weight-streaming bandwidth of each. `request` times whole reordered requests at 20 % recompute
+(graph engines, every block on the GPU) under one or more builds of the library in one process,
+alternating between them (A/B of a kernel change with the engine's own rows).
 """
 import argparse
 import sys
@@ -207,13 +210,61 @@ def bench_skinny(cfg, iters):
                   f"({nbytes / t_s / 1e9:.0f} GB/s), torch {t_t * 1e6:.1f} us ({nbytes / t_t / 1e9:.0f} GB/s)")
 
 
+def bench_request(cfg, name, n_docs, doc_len, n_sys, n_query, iters, libs, ratio=0.2):
+    """Whole reordered requests (all blocks on the GPU, graph engines, `ratio` deviation recompute)
+    under several builds of libtread_hip.so in one process: each build is loaded, an engine is
+    captured with it, and timed requests alternate between the engines. Prints the median TTFT per
+    build and the largest logits difference from the first build."""
+    import statistics
+    from pathlib import Path
+    from tread_amd import BlockStore, Engine
+    from tread_amd.model import synthetic_model
+    from tread_amd.tuning import table_for, use_tuned_gemms
+    table = table_for(name)
+    if table is not None:
+        use_tuned_gemms(tables=(table,))
+    loaded = {}
+    for p in libs:
+        _hip._lib = None
+        _hip.LIB_PATH = Path(p).resolve()
+        loaded[p] = _hip.lib()
+    model = synthetic_model(cfg, "cuda", torch.bfloat16, seed=0)
+    g = torch.Generator().manual_seed(1)
+    V = cfg.vocab_size
+    system = torch.randint(0, V, (n_sys,), generator=g).cuda()
+    docs = [torch.randint(0, V, (doc_len,), generator=g).cuda() for _ in range(n_docs)]
+    query = torch.randint(0, V, (n_query,), generator=g).cuda()
+    order = [docs[i] for i in torch.randperm(n_docs, generator=torch.Generator().manual_seed(2)).tolist()]
+    store = BlockStore(1 << 40)
+    engines, times, logits = {}, {p: [] for p in libs}, {}
+    with torch.inference_mode():
+        _hip._lib = loaded[libs[0]]
+        Engine(model, store).prefill(system, docs, query)
+        for p in libs:
+            _hip._lib = loaded[p]
+            engines[p] = Engine(model, store, graphs=True)
+            for _ in range(2):  # capture, then one replay
+                engines[p].prefill(system, order, query, ratio=ratio)
+        for _ in range(iters):
+            for p in libs:
+                _hip._lib = loaded[p]
+                out, _, st = engines[p].prefill(system, order, query, ratio=ratio)
+                times[p].append(st.t["ttft"] * 1e3)
+                logits[p] = out.float()
+    for p in libs:
+        d = (logits[p] - logits[libs[0]]).abs().max().item()
+        print(f"request[{n_sys} + {n_docs} x {doc_len} + {n_query}, ratio {ratio}] {p}: median TTFT "
+              f"{statistics.median(times[p]):.3f} ms (min {min(times[p]):.3f}), max |logits - first build| {d:.3e}")
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("kernel", choices=["assemble", "copy", "attention", "tiercopy", "deviation", "skinny"])
+    ap.add_argument("kernel", choices=["assemble", "copy", "attention", "tiercopy", "deviation", "skinny", "request"])
     ap.add_argument("--workload", default="qwen2.5-7b-32k", choices=list(WORKLOADS))
     ap.add_argument("--shape", default="recompute", choices=["recompute", "prefill", "query"])
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--sdpa", action="store_true", help="attention: also time torch's SDPA on the same inputs")
+    ap.add_argument("--libs", default="", help="request: comma-separated builds of libtread_hip.so to compare")
     args = ap.parse_args(argv)
     name, n_docs, doc_len, n_sys, n_query = WORKLOADS[args.workload]
     cfg = preset(name)
@@ -228,6 +279,9 @@ def main(argv=None):
         bench_skinny(cfg, args.iters)
     elif args.kernel == "deviation":
         bench_deviation(cfg, n_docs, doc_len, n_sys, n_query, args.iters)
+    elif args.kernel == "request":
+        libs = [p for p in args.libs.split(",") if p] or [str(_hip.LIB_PATH)]
+        bench_request(cfg, name, n_docs, doc_len, n_sys, n_query, args.iters, libs)
     else:
         bench_attention(cfg, n_docs, doc_len, n_sys, n_query, args.iters, args.shape, sdpa=args.sdpa)
     return 0
