@@ -2,16 +2,14 @@
 //
 // One streaming pass over HBM: every source row is read once and written once. Within a work unit
 // (source, layer, kv head, a span of token rows) the source rows and the destination rows are each
-// one contiguous span, so K and V move as 16-byte vectors with non-temporal loads and stores.
-//  - head_dim 128 (`rope_assemble_kernel`): a unit is 16 token rows of ONE tensor, K or V, and
-//    thread t moves chunk t of that 4 KiB span: the one-chunk-per-thread, one-stream-per-group
-//    shape of the fastest plain copy on this part (the 7B request's bytes without rotation:
-//    6.1 TB/s, against 5.4-5.8 with K and V in one group). rotate_half's partner of K chunk j is
-//    chunk j ^ 8 of the same row, i.e. lane l ^ 8 within a 16-lane DPP row (row_ror:8). The
-//    source's cos/sin table (512 B) is staged in LDS once per group: read from the cache by every
-//    thread it would be 4x the unit's own bytes (measured 730 vs 627 us per request).
-//  - head_dim 64 (`rope_assemble_pairs_kernel`): a unit is 32 token rows of K and V; each thread
-//    moves one V chunk and, on half of the threads, one K pair (j, j + hd/2).
+// one contiguous span, so K and V move as 16-byte vectors with non-temporal loads and stores. A
+// unit is 4 KiB of ONE tensor, K or V (16 token rows at head_dim 128, 32 at 64), and thread t
+// moves one 16-byte chunk of that span: the one-chunk-per-thread, one-stream-per-group shape of the
+// fastest plain copy on this part (the 7B request's bytes without rotation: 6.1 TB/s, against
+// 5.4-5.8 with K and V in one group). rotate_half's partner of a K chunk comes from another lane of
+// the same 16-lane DPP row (row_ror:8). The source's cos/sin table (HD * 4 bytes) is staged in LDS
+// once per group: read from the cache by every thread it would be 4x the unit's own bytes
+// (measured 730 vs 627 us per 7B request).
 // cos/sin come from a per-source fp32 table that the caller builds exactly as the reference's
 // rotary embedding does. The rotation keeps the reference's fp32 op order with no contraction,
 // fl(fl(x1*c) + fl(-x2*s)) and fl(fl(x2*c) + fl(x1*s)), then one RNE to bf16.
@@ -52,8 +50,7 @@ struct AsmArgs {
   int32_t n_lr;  // layers in this launch
 };
 
-// Rows per work unit: one 16-byte chunk per thread of one row span (hd 128: K or V; hd 64: the V
-// span, with the K pairs on the first half of the threads).
+// Rows per work unit: one 16-byte chunk per thread of one row span of K or V.
 template <int HD>
 constexpr int asm_rows() { return ASM_THREADS / (HD / 8); }
 
@@ -105,11 +102,16 @@ __device__ __forceinline__ uint32_t lane_xor8(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
 }
 
-// head_dim 128. Work group b is unit b / 2, its K span for even b and its V span for odd b (K
-// only, one group per unit, when the launch moves no V).
-template <int GS>
+// Work group b is unit b / 2, its K span for even b and its V span for odd b (K only, one group
+// per unit, when the launch moves no V); thread t moves one 16-byte chunk of the span's 4 KiB.
+// rotate_half's partner of K chunk j is chunk j ^ (CH / 2) of the same row; the chunks are dealt
+// so that it sits at lane l ^ 8 of the same 16-lane DPP row (row_ror:8): at head_dim 128 thread t
+// takes chunk t (16 chunks a row); at head_dim 64 (8 chunks a row) each 16-lane row takes two rows,
+// lanes 0-3 / 4-7 the first / second row's chunks 0-3 and lanes 8-11 / 12-15 their chunks 4-7 (a
+// wave still covers 1 KiB of contiguous rows).
+template <int HD, int GS>
 __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArgs a) {
-  constexpr int HD = 128, HALF = HD / 2, CH = HD / 8;  // 16 chunks per row, 16 rows per unit
+  constexpr int HALF = HD / 2, CH = HD / 8;
   const int b = blockIdx.x;
   const int bk = b >> GS;  // this group's bucket word: the first load
   const uint32_t e = (a.bucket_src[bk >> 2] >> ((bk & 3) * 8)) & 0xffu;
@@ -118,32 +120,38 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArg
   const bool is_v = has_v && (b & 1);
   const AsmUnit w = asm_unit_from<HD>(a, u, e);
   const AsmSrc& src = a.src[w.s];
-  const int c = threadIdx.x, r = c / CH;
-  const bool ok = r < w.rows;
+  const int c = threadIdx.x;
   if (is_v) {
-    if (ok) stg_nt(reinterpret_cast<u32x4_t*>(a.dv + w.doff) + c, ldg_nt(reinterpret_cast<const u32x4_t*>(src.v + w.soff) + c));
+    if (c / CH < w.rows)
+      stg_nt(reinterpret_cast<u32x4_t*>(a.dv + w.doff) + c, ldg_nt(reinterpret_cast<const u32x4_t*>(src.v + w.soff) + c));
     return;
   }
+  int sc = c;  // this thread's chunk of the K span
+  if constexpr (HD == 64) {
+    const int i = c & 15;
+    sc = ((c >> 4) * 2 + ((i >> 2) & 1)) * CH + ((i & 3) | ((i >> 3) << 2));
+  }
+  const int r = sc / CH, j = sc % CH;
+  const bool ok = r < w.rows;
   u32x4_t x = {0, 0, 0, 0};
-  if (ok) x = ldg_nt(reinterpret_cast<const u32x4_t*>(src.k + w.soff) + c);
+  if (ok) x = ldg_nt(reinterpret_cast<const u32x4_t*>(src.k + w.soff) + sc);
   if (src.delta == 0) {  // a bit copy
-    if (ok) stg_nt(reinterpret_cast<u32x4_t*>(a.dk + w.doff) + c, x);
+    if (ok) stg_nt(reinterpret_cast<u32x4_t*>(a.dk + w.doff) + sc, x);
     return;
   }
-  __shared__ f32x4_t tab_s[HALF * 2 / 4];  // (cos, sin) of the source's 64 columns
+  __shared__ f32x4_t tab_s[HALF * 2 / 4];  // (cos, sin) of the source's HALF columns
   if (c < HALF * 2 / 4) tab_s[c] = reinterpret_cast<const f32x4_t*>(a.cos_sin + (int64_t)w.s * HALF * 2)[c];
   __syncthreads();
-  const int j = c % CH;
-  const int g = (j & 7) * 4;  // columns (j & 7) * 8 .. + 7
+  const int g = (j % (CH / 2)) * 4;  // columns (j % (CH / 2)) * 8 .. + 7
   const f32x4_t t0 = tab_s[g], t1 = tab_s[g + 1], t2 = tab_s[g + 2], t3 = tab_s[g + 3];
-  u32x4_t p;  // partner chunk j ^ 8 (every lane of the row takes part, valid or not)
+  u32x4_t p;  // partner chunk j ^ (CH / 2) (every lane of the row takes part, valid or not)
 #pragma unroll
   for (int q = 0; q < 4; ++q) p[q] = lane_xor8(x[q]);
   if (!ok) return;
   const float cv[8] = {t0[0], t0[2], t1[0], t1[2], t2[0], t2[2], t3[0], t3[2]};
   const float sv[8] = {t0[1], t0[3], t1[1], t1[3], t2[1], t2[3], t3[1], t3[3]};
-  // own chunk y, partner chunk p: first half (j < 8) y c + (-p) s, second half y c + p s
-  const float sg = j < 8 ? -1.f : 1.f;
+  // own chunk y, partner chunk p: first half y c + (-p) s, second half y c + p s
+  const float sg = j < CH / 2 ? -1.f : 1.f;
   u32x4_t o;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -155,93 +163,7 @@ __global__ __launch_bounds__(ASM_THREADS) void rope_assemble_kernel(const AsmArg
       o[q] = pack_bf(yl * cl + pl * sl, yh * ch + ph * sh);
     }
   }
-  stg_nt(reinterpret_cast<u32x4_t*>(a.dk + w.doff) + c, o);
-}
-
-// head_dim 64
-template <int HD, int GS>
-__global__ __launch_bounds__(ASM_THREADS) void rope_assemble_pairs_kernel(const AsmArgs a) {
-  constexpr int HALF = HD / 2;
-  constexpr int PG = HALF / 8;               // pair groups per K row
-  constexpr int ROWS = asm_rows<HD>();       // 32 (hd 64)
-  constexpr int V_PER_T = ROWS * (HD / 8) / ASM_THREADS;  // 16-byte chunks per thread: 1
-
-  const int u = blockIdx.x;  // one group per unit
-  const int bk = u >> GS;
-  const AsmUnit w = asm_unit_from<HD>(a, u, (a.bucket_src[bk >> 2] >> ((bk & 3) * 8)) & 0xffu);
-  const int s = w.s, rows = w.rows;
-  const int64_t soff = w.soff, doff = w.doff;
-  const AsmSrc& src = a.src[s];
-  const int tid = threadIdx.x;
-  const int nvec = rows * HD / 8;  // valid 16-byte chunks of this unit's K or V span
-  const bool has_v = a.dv != nullptr;  // uniform: a K-only launch (rotate_keys) moves no V
-  const u32x4_t* vs = reinterpret_cast<const u32x4_t*>(has_v ? src.v + soff : nullptr);
-  u32x4_t* vd = reinterpret_cast<u32x4_t*>(has_v ? a.dv + doff : nullptr);
-
-  if (src.delta == 0) {  // K and V are both bit copies of one contiguous span each
-    const u32x4_t* ks = reinterpret_cast<const u32x4_t*>(src.k + soff);
-    u32x4_t* kd = reinterpret_cast<u32x4_t*>(a.dk + doff);
-    u32x4_t vb[V_PER_T], kb[V_PER_T];
-#pragma unroll
-    for (int j = 0; j < V_PER_T; ++j) {
-      int c = tid + j * ASM_THREADS;
-      if (c < nvec) {
-        if (has_v) vb[j] = ldg_nt(vs + c);
-        kb[j] = ldg_nt(ks + c);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < V_PER_T; ++j) {
-      int c = tid + j * ASM_THREADS;
-      if (c < nvec) {
-        if (has_v) stg_nt(vd + c, vb[j]);
-        stg_nt(kd + c, kb[j]);
-      }
-    }
-    return;
-  }
-
-  // every load first: V chunks, the K pair, this column group's cos/sin
-  const int r = tid / PG, c = (tid % PG) * 8;
-  const bf16_t* kr = src.k + soff + (int64_t)r * HD;
-  u32x4_t vb[V_PER_T], x1, x2;
-#pragma unroll
-  for (int j = 0; j < V_PER_T; ++j) {
-    int cc = tid + j * ASM_THREADS;
-    if (has_v && cc < nvec) vb[j] = ldg_nt(vs + cc);
-  }
-  if (r < rows) {
-    x1 = ldg_nt(reinterpret_cast<const u32x4_t*>(kr + c));
-    x2 = ldg_nt(reinterpret_cast<const u32x4_t*>(kr + c + HALF));
-  }
-  const f32x4_t* tab = reinterpret_cast<const f32x4_t*>(a.cos_sin + ((int64_t)s * HALF + c) * 2);
-  f32x4_t t0 = tab[0], t1 = tab[1], t2 = tab[2], t3 = tab[3];  // (cos, sin) of columns c..c+7
-#pragma unroll
-  for (int j = 0; j < V_PER_T; ++j) {
-    int cc = tid + j * ASM_THREADS;
-    if (has_v && cc < nvec) stg_nt(vd + cc, vb[j]);
-  }
-  if (r < rows) {
-    const float cv[8] = {t0[0], t0[2], t1[0], t1[2], t2[0], t2[2], t3[0], t3[2]};
-    const float sv[8] = {t0[1], t0[3], t1[1], t1[3], t2[1], t2[3], t3[1], t3[3]};
-    u32x4_t o1, o2;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float cl = cv[2 * w], ch = cv[2 * w + 1], sl = sv[2 * w], sh = sv[2 * w + 1];
-      const float al = lo_bf(x1[w]), ah = hi_bf(x1[w]);
-      const float bl = lo_bf(x2[w]), bh = hi_bf(x2[w]);
-      // first half: x1*cos + (-x2)*sin ; second half: x2*cos + x1*sin; each product and sum
-      // rounded to fp32 on its own, as the reference's separate torch ops do
-      {
-#pragma clang fp contract(off)
-        o1[w] = pack_bf(al * cl + (-bl) * sl, ah * ch + (-bh) * sh);
-        o2[w] = pack_bf(bl * cl + al * sl, bh * ch + ah * sh);
-      }
-    }
-    bf16_t* kd = a.dk + doff + (int64_t)r * HD;
-    stg_nt(reinterpret_cast<u32x4_t*>(kd + c), o1);
-    stg_nt(reinterpret_cast<u32x4_t*>(kd + c + HALF), o2);
-  }
+  stg_nt(reinterpret_cast<u32x4_t*>(a.dk + w.doff) + sc, o);
 }
 
 }  // namespace tread
@@ -251,9 +173,9 @@ using namespace tread;
 template <int GS>
 static void launch_gs(int head_dim, dim3 grid, dim3 block, hipStream_t s, const AsmArgs& a) {
   if (head_dim == 128)
-    hipLaunchKernelGGL(rope_assemble_kernel<GS>, grid, block, 0, s, a);
+    hipLaunchKernelGGL((rope_assemble_kernel<128, GS>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((rope_assemble_pairs_kernel<64, GS>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((rope_assemble_kernel<64, GS>), grid, block, 0, s, a);
 }
 
 static void launch_assemble(int head_dim, int gs, dim3 grid, dim3 block, hipStream_t s, const AsmArgs& a) {
@@ -315,8 +237,8 @@ extern "C" int tread_rope_assemble_bf16(const tread_src_t* srcs, int n_src, void
     }
     if (units == 0) continue;
     if (units > 0x7fffffffLL) return fail(TREAD_ERANGE, "rope_assemble: too many work units");
-    // hd 128: one work group per unit and tensor (K, V)
-    const int64_t groups = head_dim == 128 && dst_v ? 2 * units : units;
+    // one work group per unit and tensor (K, V)
+    const int64_t groups = dst_v ? 2 * units : units;
     const int gshift = asm_bucket_shift(groups), ushift = groups == units ? 0 : 1;
     if (groups > 0x7fffffffLL || gshift < 0) return fail(TREAD_ERANGE, "rope_assemble: too many work units");
     for (int b = 0, si = 0; b < ASM_BUCKETS; ++b) {  // the units of bucket b's groups
