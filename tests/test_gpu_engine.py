@@ -273,11 +273,14 @@ def test_cpu_tier_offloads_and_serves_hits(setup):
     assert list(store.blocks) == list(ostore.blocks) and list(store.cpu_blocks) == list(ostore.cpu_blocks)
 
 
-@pytest.mark.parametrize("graphs", [False, True])
-def test_host_tier_promotions_give_identical_results(setup, graphs):
+@pytest.mark.parametrize("graphs,policy", [(False, "deviation"), (True, "deviation"), (True, "boundary")])
+def test_host_tier_promotions_give_identical_results(setup, graphs, policy):
     """(d): blocks promoted from the pinned-host tier (batched layer-group DMAs, lazy per-layer
-    assembly, per-layer graph replays) give bit-identical logits to the same request served from
-    the GPU tier, on the first promotion and on the next one (pinned copies reused)."""
+    assembly, per-layer graph replays) give bit-identical logits and caches to the same request
+    served from the GPU tier, on the first promotion and on the next one (pinned copies reused).
+    With the deviation pass the docs' DMAs move layer 0 last and are queued only when a later
+    layer is first assembled (their layer 0 is recomputed, not assembled); with the boundary
+    policy layer 0 is assembled from the copies first."""
     cfg, gpu, ref = setup
     prefix, docs, query = request(cfg, seed=13, n_docs=5)
     reordered = [docs[i] for i in (3, 0, 4, 1, 2)]
@@ -286,15 +289,18 @@ def test_host_tier_promotions_give_identical_results(setup, graphs):
     one_block = max(b.nbytes for b in probe.blocks.values())
     ref_eng = Engine(gpu, BlockStore(1 << 30), graphs=graphs)
     ref_eng.prefill(on(prefix), on(docs), on(query))
-    want, _, _ = ref_eng.prefill(on(prefix), on(reordered), on(query), ratio=0.3)
+    want, wc, _ = ref_eng.prefill(on(prefix), on(reordered), on(query), ratio=0.3, policy=policy)
+    wK, wV = wc.K[..., :wc.length, :].clone(), wc.V[..., :wc.length, :].clone()
     store = BlockStore(2 * one_block, cpu_budget_bytes=1 << 30)
     eng = Engine(gpu, store, graphs=graphs)
     eng.prefill(on(prefix), on(docs), on(query))
     for rnd in range(2):
         h0 = store.stats.cpu_hits
-        got, _, st = eng.prefill(on(prefix), on(reordered), on(query), ratio=0.3)
+        got, gc, st = eng.prefill(on(prefix), on(reordered), on(query), ratio=0.3, policy=policy)
         assert st.misses == 0 and store.stats.cpu_hits - h0 >= 3, (rnd, store.stats.cpu_hits - h0)
         assert torch.equal(got, want), (rnd, (got.float() - want.float()).abs().max())
+        assert gc.length == wc.length
+        assert torch.equal(gc.K[..., :gc.length, :], wK) and torch.equal(gc.V[..., :gc.length, :], wV), rnd
     torch.cuda.synchronize()
     for b in store.cpu_blocks.values():
         b.synchronize()

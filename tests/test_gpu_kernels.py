@@ -109,7 +109,7 @@ def test_rope_assemble_more_sources_than_one_launch_holds(hd):
     assert u.max().item() == 0, (u.max(), (u > 0).sum())
 
 
-@pytest.mark.parametrize("hd,with_v", [(128, True), (64, True), (128, False)])
+@pytest.mark.parametrize("hd,with_v", [(128, True), (64, True), (128, False), (64, False)])
 def test_rope_assemble_empty_and_uneven_sources(hd, with_v):
     """Empty, one-token and long sources in one launch: a work group finds its source through the
     launch's bucket table, and here buckets hold several sources (and empty ones) as well as runs

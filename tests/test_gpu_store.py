@@ -3,6 +3,7 @@ their own stream, and the data after round trips (tread/store.py:56-125 semantic
 import pytest
 import torch
 
+from tread_amd import _hip
 from tread_amd.store import BlockStore
 
 pytestmark = pytest.mark.gpu
@@ -67,3 +68,41 @@ def test_promotions_in_a_batch_are_layer_major():
     for i, b in enumerate(got):
         b.wait()
         assert torch.equal(b.K.cpu(), data[i][0]) and torch.equal(b.V.cpu(), data[i][1])
+
+
+def test_unqueued_batch_moves_layer0_last_on_flush():
+    """batch(flush=False, layer0_last=True): nothing is queued on exit (a wait then raises instead
+    of passing on an unrecorded event); the next flush() queues the schedule with layer 0 in its
+    own group, last, so that its event landing means every group has; the data lands intact. A
+    plain batch afterwards keeps layer 0 first."""
+    L = 5
+    data = blocks(4, L=L)
+    nbytes = 2 * data[0][0].numel() * 2
+    store = BlockStore(nbytes, 1 << 30)
+    for i, (K, V) in enumerate(data):
+        store.put(f"h{i}", K.to(DEV), V.to(DEV), 0)
+    torch.cuda.synchronize()
+    store.budget = 4 * nbytes
+    with store.batch(flush=False, layer0_last=True):
+        got = [store.get(f"h{i}") for i in range(2)]
+    assert all(b.ready == [] for b in got)
+    with pytest.raises(RuntimeError):
+        got[0].wait()
+    store.flush()
+    ev = got[0].ready
+    assert len(ev) == L and all(b.ready is ev for b in got)
+    groups = _hip.layer_groups(L)
+    assert groups[0] == (0, 1) and len(groups) > 2
+    assert all(ev[0] is not ev[l] for l in range(1, L))  # layer 0 alone
+    assert store._inflight[-1][0] is ev[0]  # the schedule's last group
+    for i, b in enumerate(got):
+        b.wait()
+        assert torch.equal(b.K.cpu(), data[i][0]) and torch.equal(b.V.cpu(), data[i][1])
+    torch.cuda.synchronize()
+    store._reap()
+    assert all(b.ready is None for b in got)  # landed: resident from now on
+    with store.batch():
+        (b2,) = [store.get("h2")]
+    assert store._inflight[-1][0] is b2.ready[L - 1]  # default order: the last layers go last
+    b2.wait()
+    assert torch.equal(b2.K.cpu(), data[2][0]) and torch.equal(b2.V.cpu(), data[2][1])

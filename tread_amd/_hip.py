@@ -453,9 +453,9 @@ def layer_groups(L):
 
 def copy_layers(dsts, srcs, stream, groups, events):
     """Layer-major DMAs for blocks stacked by layer: dsts, srcs are equal-length lists of
-    contiguous [L, ...] tensors (pinned host <-> device). For each layer group (a, b) in order, the
-    slices [a, b) of every pair are queued on `stream` (one DMA per tensor), then that group's
-    torch.cuda.Event is recorded. One library call."""
+    contiguous [L, ...] tensors (pinned host <-> device). For each layer group (a, b) in the given
+    order (any order of disjoint ranges), the slices [a, b) of every pair are queued on `stream`
+    (one DMA per tensor), then that group's torch.cuda.Event is recorded. One library call."""
     import numpy as np
     n, G = len(dsts), len(groups)
     if n == 0 or G == 0:
@@ -464,7 +464,7 @@ def copy_layers(dsts, srcs, stream, groups, events):
     sb = np.empty(n, dtype=np.uint64)
     lb = np.empty(n, dtype=np.uint64)
     for i, (d, s_) in enumerate(zip(dsts, srcs)):
-        if d.shape != s_.shape or d.dtype != s_.dtype or d.shape[0] < groups[-1][1]:
+        if d.shape != s_.shape or d.dtype != s_.dtype or d.shape[0] < max(g[1] for g in groups):
             raise ValueError(f"copy_layers: pair {i} shapes {tuple(d.shape)} / {tuple(s_.shape)}")
         if not (d.is_contiguous() and s_.is_contiguous()):
             raise ValueError(f"copy_layers: pair {i} must be contiguous")

@@ -65,14 +65,24 @@ def model_sig(model):
 
 
 class _Assembly:
-    """Rotate+gather of the request's blocks into the cache; per-layer for in-flight blocks."""
+    """Rotate+gather of the request's blocks into the cache; per-layer for in-flight blocks.
 
-    def __init__(self, P, K, V, sources):
+    `store`: flushed before a layer of an in-flight block is read (its DMAs may have been left
+    unqueued, see BlockStore.batch). `skip0`: indices of sources whose layer 0 the request
+    recomputes in place (the deviation pass splices fresh k/v into every doc row of layer 0), so
+    layer 0 of those in flight is not assembled and their layer-0 DMAs are not waited for."""
+
+    def __init__(self, P, K, V, sources, store=None, skip0=()):
         self.P, self.K, self.V = P, K, V
+        self.store = store
         ready = [(b.K, b.V, off, delta) for b, off, delta in sources if getattr(b, "ready", None) is None]
         self.pending = [(b, off, delta) for b, off, delta in sources if getattr(b, "ready", None) is not None]
+        skip = set(skip0)
+        self.pending0 = self.pending if not skip else [
+            (b, off, delta) for i, (b, off, delta) in enumerate(sources)
+            if getattr(b, "ready", None) is not None and i not in skip]
         self.done = [False] * P.L
-        self.table = None
+        self.tables = {}
         self.waited = set()  # ids of copy events the current stream already waits on
         if ready:
             _hip.rope_assemble(ready, K, V, P.inv_freq)
@@ -82,10 +92,13 @@ class _Assembly:
     def ensure(self, l):
         if self.done[l]:
             return
+        pend = self.pending0 if l == 0 else self.pending
+        if self.store is not None and any(b.ready is not None and not b.ready for b, _, _ in pend):
+            self.store.flush()  # their DMAs were left unqueued: queue them now
         # blocks promoted in one batch share their layer-group events: one stream wait per event
         # (each wait is a barrier packet the GPU processes in order)
         cur = torch.cuda.current_stream()
-        for b, _, _ in self.pending:
+        for b, _, _ in pend:
             e = b.ready[l] if b.ready is not None else None
             if e is not None and id(e) not in self.waited:
                 cur.wait_event(e)
@@ -93,11 +106,15 @@ class _Assembly:
         # the following layers whose copies landed with layer l's (the same event for every pending
         # block) are assembled by the same launch
         hi = l + 1
-        while hi < self.P.L and not self.done[hi] and all(
-                b.ready is None or (b.ready[hi] is b.ready[l]) for b, _, _ in self.pending):
-            hi += 1
-        self.table = _hip.rope_assemble([(b.K, b.V, off, delta) for b, off, delta in self.pending], self.K, self.V,
-                                        self.P.inv_freq, layer_lo=l, layer_hi=hi, table=self.table)
+        if pend is self.pending:  # (layer 0 of a skipping request is assembled alone)
+            while hi < self.P.L and not self.done[hi] and all(
+                    b.ready is None or (b.ready[hi] is b.ready[l]) for b, _, _ in pend):
+                hi += 1
+        if pend:
+            key = id(pend)
+            self.tables[key] = _hip.rope_assemble([(b.K, b.V, off, delta) for b, off, delta in pend], self.K,
+                                                  self.V, self.P.inv_freq, layer_lo=l, layer_hi=hi,
+                                                  table=self.tables.get(key))
         for x in range(l, hi):
             self.done[x] = True
 
@@ -194,11 +211,18 @@ class Engine:
         if prefix_ids.device.type != "cpu":  # one device-to-host copy for every key's ids
             hp, *hd = torch.cat([prefix_ids] + list(docs)).to("cpu", torch.int64).split(
                 [len(prefix_ids)] + [len(d) for d in docs])
+        budget = select(ratio, docs)[1] if (ratio > 0 and docs) else 0
+        # With the deviation pass, layer 0 of every doc row is recomputed in place: the docs'
+        # host-tier copies move layer 0 last, and their DMAs are queued once the deviation pass's
+        # layer 0 is launched (the first assembly of a later layer flushes the store), so that
+        # the host time of queueing them runs beside GPU work instead of before it.
+        recompute0 = budget > 0 and policy == "deviation"
         with self.store.batch():  # host-tier hits share one layer-major H2D schedule
             pkey = block_key(*self.sig, namespace, "prefix", prefix_ids if hp is None else hp)
             dkeys = [block_key(*self.sig, pkey, d) for d in (docs if hd is None else hd)]
             self.store.prefetch([pkey] + dkeys)  # disk-tier files: read and verified in parallel
             pkey, pb = self.prefix_block(prefix_ids, st, namespace, host_ids=hp, key=pkey)
+        with self.store.batch(flush=not recompute0, layer0_last=recompute0):
             blocks = self.doc_blocks(pkey, pb, docs, st, host_docs=hd, keys=dkeys)
         Pn = pb.n_tokens
         T = Pn + sum(len(d) for d in docs)
@@ -206,7 +230,6 @@ class Engine:
         dev = prefix_ids.device
         graph = None
         if self.runner is not None and self.runner.worth_it(T):
-            budget = select(ratio, docs)[1] if (ratio > 0 and docs) else 0
             if budget > 0:
                 start = 1 if policy == "deviation" else 0
                 graph = self.runner.cache_for(start, budget, T, Nq, dev, room=Nq + reserve,
@@ -223,7 +246,8 @@ class Engine:
             sources.append((b, offset, offset - b.base))
             offset += len(d)
         cands = list(torch.arange(Pn, T, device=dev).split([len(d) for d in docs])) if docs else []
-        asm = _Assembly(self.P, K, V, sources)
+        asm = _Assembly(self.P, K, V, sources, store=self.store,
+                        skip0=range(1, len(sources)) if recompute0 else ())
         hook = asm.ensure if asm.pending else None  # None: nothing to wait for between layers
         Kl, Vl = K.unbind(0), V.unbind(0)
         self._sync()
@@ -252,6 +276,7 @@ class Engine:
             R = make_rows(self.P, torch.arange(T, T + Nq, device=dev))
             h, d = run_layers(self.P, embed(self.P, query_ids), None, R, Kl, Vl, range(self.P.L), hook=hook)
             logits = final_logits(self.P, h, d)
+        self.store.flush()  # nothing is left unqueued past the request (a no-op after any later layer)
         self._sync()
         t3 = time.perf_counter()
         st.t = dict(assemble=t1 - t0, blend=t2 - t1, query=t3 - t2, ttft=t3 - t0)

@@ -20,6 +20,7 @@ from collections import OrderedDict
 
 import torch
 
+from tread_amd import _hip
 from tread_amd.forward import alloc_cache, embed, make_rows, norm_logits, run_layers
 
 
@@ -84,16 +85,18 @@ class _QueryGraph:
 
 
 class _Graph:
-    """The recompute loop of one bucket, captured as one graph per group of `seg` layers that
-    chain through static hidden-state tensors: a replay can then wait for each layer's host-tier
-    copies (and assemble them) right before that layer, instead of before the whole loop.
+    """The recompute loop of one bucket, captured as one graph per segment of layers, the segments
+    chaining through static hidden-state tensors: a replay can then wait for each segment's
+    host-tier copies (and assemble them) right before it, instead of before the whole loop. The
+    segments are the layer groups the store's host-tier copies arrive in (`seg=None`), so a replay
+    with copies in flight waits once per group; `seg=k` cuts every k layers instead.
 
     Rows of a replay: the n recomputed positions, then (with nq > 0) nq query slots at T, T+1, ...
     whose forward rides along (the last segment ends with the final norm + lm_head of query slot
     `last`), then padding. Padded rows see no key (key end -1) and write their k/v to spare rows
     no real row reads."""
 
-    def __init__(self, P, start, nb, Tb, t_cap, device, trim_last, seg=1, nq=0):
+    def __init__(self, P, start, nb, Tb, t_cap, device, trim_last, seg=None, nq=0):
         self.t_cap = t_cap
         self.generation = 0  # bumped whenever a request claims this bucket's cache
         self.queries = {}  # nq -> _QueryGraph over this bucket's cache
@@ -110,7 +113,10 @@ class _Graph:
         self.nb, self.Tb, self.start = nb, Tb, start
         self.pool = torch.cuda.graph_pool_handle()
         layers = list(range(start, P.L))
-        groups = [layers[i:i + seg] for i in range(0, len(layers), seg)]
+        if seg is None:
+            groups = [list(range(max(a, start), b)) for a, b in _hip.layer_groups(P.L) if b > start]
+        else:
+            groups = [layers[i:i + seg] for i in range(0, len(layers), seg)]
 
         def loop(ls, first, last, prev, carry):
             """Layers ls of the loop; the first group builds the row tables, later ones continue
@@ -177,7 +183,7 @@ class SubsetRunner:
     the bucket and back; the engine assembles into its buckets instead, copies nothing, and
     constructs its runner with max_ctx=None."""
 
-    def __init__(self, model, max_graphs=4, max_ctx=2048, trim_last=True, seg=1, max_query_buckets=2):
+    def __init__(self, model, max_graphs=4, max_ctx=2048, trim_last=True, seg=None, max_query_buckets=2):
         from tread_amd.blend import prepared
         self.model = model
         self.P = prepared(model)

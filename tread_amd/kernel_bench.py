@@ -7,6 +7,7 @@
     python -m tread_amd.kernel_bench deviation [--workload qwen2.5-7b-32k]
     python -m tread_amd.kernel_bench skinny    [--workload qwen2.5-7b-32k]
     python -m tread_amd.kernel_bench request   [--workload qwen2.5-7b-32k] [--libs a.so,b.so]
+    python -m tread_amd.kernel_bench tier      [--workload qwen2.5-1.5b-16k] [--gpu-docs 8]
 
 `assemble` launches the fused re-rotate+assemble kernel on one request's blocks (prefix + every
 doc, each doc shifted); `copy` copies the same number of bytes with torch (the calibration for
@@ -22,7 +23,11 @@ against the assembled layer-1 cache) and selects the top 20% of them, each launc
 1, 8 and 32 token rows through the skinny-linear kernel and through torch's GEMM, and reports the
 weight-streaming bandwidth of each. `request` times whole reordered requests at 20 % recompute
 (graph engines, every block on the GPU) under one or more builds of the library in one process,
-alternating between them (A/B of a kernel change with the engine's own rows).
+alternating between them (A/B of a kernel change with the engine's own rows). `tier` runs
+reordered requests whose blocks come from the pinned-host tier (the GPU tier holds the prefix and
+`--gpu-docs` doc blocks, so under LRU every block of a request is promoted) and prints, per
+request, when each copy schedule was queued, when each of its layer groups landed, and when the
+compute stream reached each layer's assembly and how long it waited there.
 """
 import argparse
 import sys
@@ -257,14 +262,84 @@ def bench_request(cfg, name, n_docs, doc_len, n_sys, n_query, iters, libs, ratio
               f"{statistics.median(times[p]):.3f} ms (min {min(times[p]):.3f}), max |logits - first build| {d:.3e}")
 
 
+def bench_tier(cfg, name, n_docs, doc_len, n_sys, n_query, iters, gpu_docs, ratio=0.2):
+    """Timeline of host-tier requests (graph engine, `ratio` deviation recompute): GPU times from
+    an event recorded as the request begins; host times from the same point."""
+    import time
+    from tread_amd import BlockStore, Engine
+    from tread_amd import engine as E
+    from tread_amd.model import synthetic_model
+    from tread_amd.tuning import table_for, use_tuned_gemms
+    table = table_for(name)
+    if table is not None:
+        use_tuned_gemms(tables=(table,))
+    model = synthetic_model(cfg, "cuda", torch.bfloat16, seed=0)
+    g = torch.Generator().manual_seed(1)
+    V = cfg.vocab_size
+    system = torch.randint(0, V, (n_sys,), generator=g).cuda()
+    docs = [torch.randint(0, V, (doc_len,), generator=g).cuda() for _ in range(n_docs)]
+    query = torch.randint(0, V, (n_query,), generator=g).cuda()
+    order = [docs[i] for i in torch.randperm(n_docs, generator=torch.Generator().manual_seed(2)).tolist()]
+    per_token = 2 * cfg.num_hidden_layers * cfg.num_key_value_heads * cfg.head_dim * 2
+    store = BlockStore(per_token * (n_sys + gpu_docs * doc_len), 1 << 40)
+    store.event_timing = True
+    rec = {"sched": [], "layers": []}
+    orig_copy, orig_ensure = _hip.copy_layers, E._Assembly.ensure
+
+    def copy_layers(dsts, srcs, stream, groups, events):
+        rec["sched"].append((groups, events, time.perf_counter(), len(dsts)))
+        return orig_copy(dsts, srcs, stream, groups, events)
+
+    def ensure(self, l):
+        if self.done[l]:
+            return
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        orig_ensure(self, l)
+        b.record()
+        rec["layers"].append((l, a, b))
+
+    _hip.copy_layers, E._Assembly.ensure = copy_layers, ensure
+    try:
+        with torch.inference_mode():
+            eng = Engine(model, store, graphs=True)
+            eng.prefill(system, docs, query)
+            for _ in range(2):
+                eng.prefill(system, order, query, ratio=ratio)
+            for it in range(iters):
+                rec["sched"], rec["layers"] = [], []
+                torch.cuda.synchronize()
+                t0 = torch.cuda.Event(enable_timing=True)
+                t0.record()
+                h0 = time.perf_counter()
+                _, _, st = eng.prefill(system, order, query, ratio=ratio)
+                t1 = torch.cuda.Event(enable_timing=True)
+                t1.record()
+                t1.synchronize()
+                print(f"request {it}: TTFT {st.t['ttft'] * 1e3:.2f} ms (stages " +
+                      ", ".join(f"{k} {v * 1e3:.2f}" for k, v in st.t.items() if k != "ttft") +
+                      f"), GPU span {t0.elapsed_time(t1):.2f} ms, {st.hits} hits")
+                for groups, events, hq, n in rec["sched"]:
+                    landed = ", ".join(f"{a}-{b - 1}: {t0.elapsed_time(e):.2f}" for (a, b), e in zip(groups, events))
+                    print(f"  schedule of {n} tensors queued at host +{(hq - h0) * 1e3:.2f} ms; "
+                          f"groups landed (ms): {landed}")
+                print("  assembly of layer l (compute stream reaches it at ms, waits + assembles ms): " +
+                      ", ".join(f"{l}: {t0.elapsed_time(a):.2f} +{a.elapsed_time(b):.3f}"
+                                for l, a, b in rec["layers"]))
+    finally:
+        _hip.copy_layers, E._Assembly.ensure = orig_copy, orig_ensure
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("kernel", choices=["assemble", "copy", "attention", "tiercopy", "deviation", "skinny", "request"])
+    ap.add_argument("kernel", choices=["assemble", "copy", "attention", "tiercopy", "deviation", "skinny", "request",
+                                       "tier"])
     ap.add_argument("--workload", default="qwen2.5-7b-32k", choices=list(WORKLOADS))
     ap.add_argument("--shape", default="recompute", choices=["recompute", "prefill", "query"])
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--sdpa", action="store_true", help="attention: also time torch's SDPA on the same inputs")
     ap.add_argument("--libs", default="", help="request: comma-separated builds of libtread_hip.so to compare")
+    ap.add_argument("--gpu-docs", type=int, default=8, help="tier: doc blocks the GPU tier holds")
     args = ap.parse_args(argv)
     name, n_docs, doc_len, n_sys, n_query = WORKLOADS[args.workload]
     cfg = preset(name)
@@ -279,6 +354,8 @@ def main(argv=None):
         bench_skinny(cfg, args.iters)
     elif args.kernel == "deviation":
         bench_deviation(cfg, n_docs, doc_len, n_sys, n_query, args.iters)
+    elif args.kernel == "tier":
+        bench_tier(cfg, name, n_docs, doc_len, n_sys, n_query, min(args.iters, 5), args.gpu_docs)
     elif args.kernel == "request":
         libs = [p for p in args.libs.split(",") if p] or [str(_hip.LIB_PATH)]
         bench_request(cfg, name, n_docs, doc_len, n_sys, n_query, args.iters, libs)

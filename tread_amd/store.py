@@ -9,7 +9,9 @@ at (`base`). What differs is how bytes move between tiers:
     consumers wait on those events (`Block.wait`) on their own stream, so the copy of layer l
     overlaps whatever runs before layer l is needed. Lookups made inside `batch()` share one
     schedule: group 0 of every promoted block, then group 1, ... so that the first layers of all
-    blocks land first;
+    blocks land first (layer 0 last for a request that recomputes it; the schedule can also be
+    left for a later flush(), so that its host-side queueing runs after the caller's first GPU
+    work is launched);
   - an eviction (store.py:99-115) queues a D2H DMA into freshly allocated pinned memory on a
     second stream, after the producing stream's work (and after the block's own H2D if it was
     promoted in the same batch), instead of a synchronous copy + re-pin. The evicted GPU tensors
@@ -83,6 +85,8 @@ class Block:
         """Make `stream` (default: current) wait until the GPU copy of `layers` has landed."""
         if self.ready is None:
             return
+        if not self.ready:
+            raise RuntimeError("Block: its DMAs are not queued yet; flush() the store first")
         s = stream or torch.cuda.current_stream()
         seen = set()  # layers of one copy group share its event: one wait each
         for l in (range(len(self.ready)) if layers is None else layers):
@@ -95,6 +99,8 @@ class Block:
         if self.host_ready is not None:
             self.host_ready.synchronize()
         if self.ready is not None:
+            if not self.ready:
+                raise RuntimeError("Block: its DMAs are not queued yet; flush() the store first")
             for e in self.ready:
                 e.synchronize()
 
@@ -163,6 +169,9 @@ class BlockStore:
         self._inflight = []
         self._batch = 0
         self._h2d = []  # (Block, host K, host V): promotions whose DMAs are not queued yet
+        self._h2d_after = None  # (event, promotions): the current stream's state at an unqueued batch's exit
+        self._h2d_layer0_last = False  # the pending schedule moves layer 0 last
+        self.event_timing = False  # copy-group events with timing (for timelines; slower to record)
         self._d2h = []  # (GPU Block, host Block): evictions whose DMAs are not queued yet
 
     def _reap(self):
@@ -173,7 +182,7 @@ class BlockStore:
             for e, refs, blocks in self._inflight:
                 if e.query():
                     for b in blocks:
-                        if b.ready is not None and b.ready and b.ready[-1] is e:
+                        if b.ready is not None and any(x is e for x in b.ready):
                             b.ready = None
                 else:
                     keep.append((e, refs, blocks))
@@ -191,41 +200,68 @@ class BlockStore:
         return self._stream("h2d", device)
 
     @contextmanager
-    def batch(self):
+    def batch(self, flush=True, layer0_last=False):
         """Lookups inside the block share one layer-major H2D schedule, queued on exit (or at an
-        explicit `flush()`, which a caller must make before it reads any block obtained inside)."""
+        explicit `flush()`, which a caller must make before it reads any block obtained inside).
+        flush=False leaves the schedule unqueued on exit, for the next flush(): a caller with GPU
+        work to launch first hides the host time of queueing the DMAs behind that work. The
+        schedule's DMAs still start after the work the current stream held at the batch's exit
+        (the promoted blocks' fresh allocations may reuse memory that work released), not after
+        the work launched before the flush. layer0_last: the schedule moves layer 0 last, for a
+        request that recomputes layer 0 of these blocks and reads layer 1 first."""
         self._batch += 1
+        if layer0_last:
+            self._h2d_layer0_last = True
         try:
             yield self
         finally:
             self._batch -= 1
             if self._batch == 0:
                 self._staged.clear()
-                self.flush()
+                if not self._h2d:
+                    self._h2d_layer0_last = False  # nothing promoted: no schedule to order
+                if flush:
+                    self.flush()
+                elif self._h2d:
+                    cur = torch.cuda.current_stream(self._h2d[0][0].K.device)
+                    e = torch.cuda.Event()
+                    e.record(cur)
+                    self._h2d_after = (e, len(self._h2d))
 
     def flush(self):
         """Queue the pending DMAs: promotions layer-major on the H2D stream, then evictions on the
         D2H stream."""
         if self._h2d:
             pend, self._h2d = self._h2d, []
+            after, self._h2d_after = self._h2d_after, None
+            layer0_last, self._h2d_layer0_last = self._h2d_layer0_last, False
             dev = pend[0][0].K.device
             cur = torch.cuda.current_stream(dev)
             s = self.copy_stream(dev)
-            s.wait_stream(cur)  # the fresh allocations may reuse memory the current stream released
+            # the fresh allocations may reuse memory the current stream released: wait for the work
+            # it held when they were made (a batch left unqueued recorded that point on exit)
+            if after is not None and after[1] == len(pend):
+                s.wait_event(after[0])
+            else:
+                s.wait_stream(cur)
             for _, hK, hV in pend:  # host buffers filled by a queued D2H (evicted earlier)
                 if getattr(hK, "_tread_ready", None) is not None:
                     s.wait_event(hK._tread_ready)
             L = pend[0][0].K.shape[0]
             groups = _hip.layer_groups(L)
-            gev = [torch.cuda.Event() for _ in groups]
+            if layer0_last and len(groups) > 1:
+                groups = groups[1:] + groups[:1]
+            gev = [torch.cuda.Event(enable_timing=self.event_timing) for _ in groups]
             _hip.copy_layers([t for b, _, _ in pend for t in (b.K, b.V)], [t for _, hK, hV in pend for t in (hK, hV)],
                              s, groups, gev)
-            events = [e for (a, b_), e in zip(groups, gev) for _ in range(a, b_)]  # per layer
+            group_of = {l: e for (a, b_), e in zip(groups, gev) for l in range(a, b_)}
+            events = [group_of[l] for l in range(L)]  # per layer
             for b, hK, hV in pend:
                 b.K.record_stream(s)
                 b.V.record_stream(s)
                 b.ready = events
-            self._inflight.append((events[-1], tuple(t for _, hK, hV in pend for t in (hK, hV)),
+            # the schedule's last group: once it has landed, every DMA of the schedule has
+            self._inflight.append((gev[-1], tuple(t for _, hK, hV in pend for t in (hK, hV)),
                                    tuple(b for b, _, _ in pend)))
         if self._d2h:
             pend, self._d2h = self._d2h, []
@@ -236,8 +272,9 @@ class BlockStore:
         dev = gb.K.device
         s = self._stream("d2h", dev)
         s.wait_stream(torch.cuda.current_stream(dev))  # the block's producer lands first
-        if gb.ready is not None:
-            s.wait_event(gb.ready[-1])  # and its own promotion
+        if gb.ready is not None:  # and its own promotion (one wait per layer group)
+            for e in {id(x): x for x in gb.ready}.values():
+                s.wait_event(e)
         _hip.copy_async(hb.K, gb.K, s)
         _hip.copy_async(hb.V, gb.V, s)
         e = torch.cuda.Event()
