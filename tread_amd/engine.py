@@ -7,8 +7,10 @@ P, cached under a key chained on the prefix key, and re-rotated to wherever it l
 Same API, keys, hit/miss accounting and stage timings as the reference; what runs underneath:
   - assembly: ONE fused HIP launch rotates every doc block by (offset - base) and gathers it,
     with the prefix block, into a preallocated [L, 1, kv, T + Nq, hd] cache (kernel (a)).
-    Blocks still arriving from the host tier are assembled per layer, right before the layer is
-    first read, after waiting that layer's copy event (overlap of DMA and compute);
+    Blocks still arriving from the host tier are assembled per layer group, right before the
+    group is first read, after waiting that group's copy event (overlap of DMA and compute); with
+    the deviation pass, the docs' layer 0 is recomputed rather than assembled, so their copies
+    move layer 0 last and are queued once the pass's layer 0 is launched;
   - blend: deviation pass + top-k (kernel (b)) and the recompute loop with the MFMA attention
     (kernel (c)), eager or replayed from a hipGraph whose static buffer is the cache itself;
   - query: the query rows are appended in place at rows T.. of the same cache (no cat/copy).

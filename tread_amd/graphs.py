@@ -13,8 +13,9 @@ the GEMMs their rows but no attention.
 Each bucket holds one [L, 1, kv, t_cap, hd] K/V pair; the cache returned by the engine aliases
 it and stays valid until the next request claims the same bucket (the bucket's generation counter
 then moves on and the old cache raises on access; `KVCache.detach()` keeps a copy). The loop is captured as one
-graph per layer (chained through static hidden-state tensors), so a replay waits for a layer's
-host-tier copies only right before that layer: the block-tier DMAs overlap the recompute.
+graph per layer group of the block store's host-tier copies (chained through static hidden-state
+tensors), so a replay waits for a group's copies only right before that group: the block-tier
+DMAs overlap the recompute. With no copy in flight the same loop replays as one graph.
 """
 from collections import OrderedDict
 
