@@ -410,13 +410,13 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
     bf16x8_t kf[NK];
     static_for<RING>([&](auto I) {
       constexpr int i = decltype(I)::value;
-      kf[i] = lds_read128<(i / KS) * 32 * HD * 2>(kaddr[i % KS] + ko);
+      kf[i] = lds_read128<(i % NKB) * 32 * HD * 2>(kaddr[i / NKB] + ko);
     });
     static_for<NK>([&](auto I) {
       constexpr int i = decltype(I)::value;
       constexpr int k_after = (i + RING - 1 < NK - 1 ? i + RING - 1 : NK - 1) - i;
       lgkm_wait<k_after>(kf[i]);
-      constexpr int kb = i / KS, st = i % KS;
+      constexpr int kb = i % NKB, st = i / NKB;
       if constexpr (st == 0) {
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i], qf[st], mneg, 0, 0, 0);
       } else {
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
       }
       if constexpr (i + RING < NK) {
         constexpr int m = i + RING;
-        kf[m] = lds_read128<(m / KS) * 32 * HD * 2>(kaddr[m % KS] + ko);
+        kf[m] = lds_read128<(m % NKB) * 32 * HD * 2>(kaddr[m / NKB] + ko);
       }
     });
   };
