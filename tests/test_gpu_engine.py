@@ -307,6 +307,30 @@ def test_host_tier_promotions_give_identical_results(setup, graphs, policy):
         assert b.K.is_pinned()
 
 
+def test_host_tier_with_cold_docs_in_one_request(setup):
+    """A deviation request whose docs come partly from the pinned-host tier and partly cold (packed
+    prefill inside the lookups, which queues the docs' left-unqueued copies early): logits, cache
+    and counters equal to the same requests against a store that keeps every block on the GPU."""
+    cfg, gpu, ref = setup
+    prefix, docs, query = request(cfg, seed=17, n_docs=6)
+    probe = BlockStore(1 << 30)
+    Engine(gpu, probe).prefill(on(prefix), on(docs[:4]), on(query))
+    one_block = max(b.nbytes for b in probe.blocks.values())
+    order = [docs[i] for i in (2, 4, 0, 5, 3, 1)]  # 4 and 5 are cold
+    out = {}
+    for name, store in (("gpu", BlockStore(1 << 30)), ("tier", BlockStore(2 * one_block, cpu_budget_bytes=1 << 30))):
+        eng = Engine(gpu, store, graphs=True)
+        eng.prefill(on(prefix), on(docs[:4]), on(query))
+        lg, c, st = eng.prefill(on(prefix), on(order), on(query), ratio=0.3)
+        out[name] = (lg, c.K[..., :c.length, :].clone(), c.V[..., :c.length, :].clone(), st.hits, st.misses,
+                     st.tokens_prefilled, store.stats.cpu_hits)
+    g, t = out["gpu"], out["tier"]
+    assert t[3:6] == g[3:6] and g[4] == 2, (g[3:6], t[3:6])
+    assert t[6] >= 2  # some docs came back from the host tier
+    assert torch.equal(t[0], g[0]), (t[0].float() - g[0].float()).abs().max()
+    assert torch.equal(t[1], g[1]) and torch.equal(t[2], g[2])
+
+
 def test_block_key_depends_on_prefix(setup):
     cfg, gpu, ref = setup
     prefix, docs, query = request(cfg, seed=9)
