@@ -208,6 +208,8 @@ __global__ __launch_bounds__(ATT_THREADS) void subset_attn_kernel(const AttnArgs
   constexpr int DB = HD / 32;   // 32-row d blocks of O^T
   constexpr int KCH = HD / 8;   // 16-byte chunks per K/V row
   constexpr int K_LD = BK * KCH / ATT_THREADS;  // K (and V) 16-byte chunks per thread per tile
+  static_assert(BK * KCH % ATT_THREADS == 0, "a tile's chunks split evenly over the threads");
+  static_assert(BK % 32 == 0 && SM::BUF * ATT_NBUF * 2 <= 160 * 1024, "key tile size");
   extern __shared__ __align__(16) bf16_t smem[];
   __shared__ int red[4][ATT_WAVES];
 
