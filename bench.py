@@ -33,9 +33,9 @@ MEASURED_ASSEMBLE_TRAFFIC = {"qwen2.5-7b-32k": 3677757000}
 ASSEMBLE_TRAFFIC_SOURCE = "profiles/rope_assemble_qwen2.5-7b-32k.md (PMC passes of the current kernel)"
 # HBM bytes per recompute attention call (subset_attn_kernel + attn_halves_kernel), the same two
 # passes and factors on the 6 400-row recompute shape of this workload
-# (`python3 -m tread_amd.kernel_bench attention --shape recompute`): 484.5 + 49.1 MB read,
+# (`python3 -m tread_amd.kernel_bench attention --shape recompute`): 473.7 + 49.1 MB read,
 # 90.2 + 11.5 MB written
-MEASURED_ATTENTION_TRAFFIC = {"qwen2.5-7b-32k": 635233536}
+MEASURED_ATTENTION_TRAFFIC = {"qwen2.5-7b-32k": 624431360}
 ATTENTION_TRAFFIC_SOURCE = "profiles/subset_attn_qwen2.5-7b-32k.md (PMC passes of the current kernel)"
 # doc blocks the GPU tier holds (with the prefix block); the rest spill to the pinned-host tier
 # and are copied back per request on the store's copy streams (None: everything stays on the GPU)
