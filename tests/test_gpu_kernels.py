@@ -547,6 +547,12 @@ CASES = [
     (28, 4, 128, 100, 2, "query"),     # one slice: normalised output written directly
     (6, 3, 64, 900, 5, "subset"),      # rows scattered over the cache: per-row key ends mid-tile
     (8, 2, 128, 2000, 4, "segfew"),    # block-diagonal visibility on a few rows
+    # key ends (and segment starts) on every side of every 32-key boundary, so of every key tile
+    # the kernels use (96 keys at head_dim 128, 128 at 64), and a partial last tile
+    (8, 2, 128, 1000, 90, "tiles"),
+    (14, 2, 64, 1000, 90, "tiles"),
+    (8, 2, 128, 1000, 48, "tileseg"),
+    (14, 2, 64, 1000, 48, "tileseg"),
 ]
 
 
@@ -567,6 +573,15 @@ def test_subset_attention_vs_textbook(hq, hkv, hd, t_cap, n, kind):
         kend = torch.arange(n)
     elif kind == "query":  # the query rows at the end of the cache
         kend = torch.arange(t_cap - n, t_cap)
+    elif kind == "tiles":  # key ends at 32 m - 1, 32 m, 32 m + 1
+        ends = sorted({32 * m + d for m in range(1, 32) for d in (-1, 0, 1) if 32 * m + d < t_cap})
+        kend = torch.tensor(ends[:n])
+    elif kind == "tileseg":  # shared prefix ending at a tile edge - 1, segments starting at edges
+        n_shared = 95
+        pairs = [(s0, s0 + ln) for s0 in (96, 127, 128, 129, 191, 192, 288, 289)
+                 for ln in (0, 31, 32, 95, 96, 200) if s0 + ln < t_cap]
+        kseg = torch.tensor([a for a, _ in pairs][:n])
+        kend = torch.tensor([b for _, b in pairs][:n])
     elif kind == "segfew":  # a few rows of packed docs: shared prefix + own segment
         n_shared = 40
         kend = torch.tensor([60, 300, 1210, 1999])[:n]
