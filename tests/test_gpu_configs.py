@@ -3,17 +3,17 @@
 Two oracle backends: the oracle's torch code on the CPU (its home) and the same code run a second
 time on the MI355X (hipBLASLt GEMMs, torch's memory-efficient attention kernel: the reference's own
 path as it runs on a GPU). Measured on MI355X, the two backends of the reference's path are
-themselves KL 1.2e-4 apart at the 0.5B 8k request and 4.8e-4 at the 1.5B 16k one (8.4e-5 at the
+themselves KL 1.3e-4 apart at the 0.5B 8k request and 4.8e-4 at the 1.5B 16k one (7.9e-5 at the
 7B width with 3 layers), and each is 1e-4 to 5e-4 from the fp32 truth of the same weights: a KL
 of 1e-4 to the reference is below what the reference reproduces across its own backends, so no
 bf16 implementation with other kernels can be held to it. The logits bars, on one selection:
 - KL(oracle on either backend, ours) <= max(1e-4, 2 x KL(oracle CPU, oracle GPU)): within twice
-  the reference's own cross-backend distance (measured: 0.96-1.6x);
+  the reference's own cross-backend distance (measured: 0.90-1.89x);
 - KL(fp32 truth, ours) <= 1.25 x min(KL(fp32 truth, oracle CPU), KL(fp32 truth, oracle GPU)) +
-  1e-5: no less accurate than the reference's bf16 path (measured: 0.96-1.13x of the oracle's);
+  1e-5: about as accurate as the reference's bf16 path (measured: 0.96-1.24x of the oracle's);
 - where only the GPU backend runs (the 70B width), KL(oracle GPU, ours) <= 0.5 x KL(fp32 truth,
   oracle GPU): ours differs from the reference by less than half the reference's own bf16 error
-  (measured 0.28x).
+  (measured 0.26x).
 Selections: equal to each oracle's except candidates whose oracle score lies within 2 bf16 ulps
 of its selection threshold (printed: how many differ and the largest gap).
 
